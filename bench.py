@@ -1,0 +1,246 @@
+"""Benchmark of the FP8 quantized inference hot path on one MI355X.
+
+One step of the hot path = the three kernels BASELINE names, each on its own
+synthetic workload with inputs resident in HBM:
+  * FP8 linear at the north-star shape [10800 x 3072] x [3072 x 12288]
+    (per-token activation quant + row/col-scaled FP8 GEMM with bias, GELU-tanh)
+  * FP8 KV quantize-on-write, config 2: K, V [1, 24, 10800, 128]
+  * FP8-KV chunk attention, config 3: Q [1, 24, 10800, 128] over 86400 cached tokens
+``value`` is the FP8 linear's TFLOP/s (the metric's headline); the attention
+ms / GB/s and the KV-write GB/s ride along in the same JSON line, as does the
+config-1 linear. Timing uses HIP events on the stream the kernels run on.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense BF16 MFMA
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+
+# Algorithmic work (see DESIGN.md "Measurement").
+NS_M, NS_K, NS_N = 10800, 3072, 12288
+C1_M, C1_K, C1_N = 4096, 3072, 3072
+KV_H, KV_L, KV_D = 24, 10800, 128
+ATT_CHUNKS = 8
+
+
+def gemm_flops(m, k, n):
+    return 2.0 * m * k * n
+
+
+def kv_write_bytes(h=KV_H, l=KV_L, d=KV_D):
+    rows = 2 * h * l                     # K and V rows
+    return rows * d * 2 + rows * d + rows * 4   # bf16 in, e4m3 out, fp32 scale out
+
+
+def attn_flops(h, lq, lk, d):
+    return 4.0 * h * lq * lk * d
+
+
+def attn_unique_bytes(h, lq, lk, d):
+    return h * lq * d * 2 * 2 + 2 * h * lk * d + 2 * h * lk * 4   # Q + O bf16, K/V codes, scales
+
+
+def time_loop(fn, steps, warmup, stream=None):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream() if stream is None else stream
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(s)
+    for _ in range(steps):
+        fn()
+    end.record(s)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps   # ms per call
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the hot path's multi-GPU sharding is design-only (DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = importlib.import_module("hy-nomas_amd")
+    ops = pkg.ops
+    kvc = importlib.import_module("hy-nomas_amd.fp8_kv_cache")
+    ca = importlib.import_module("hy-nomas_amd.cache_attention")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    # ---------------- FP8 linear, north-star shape
+    g = torch.Generator(device=dev).manual_seed(1234)
+    x = torch.randn(NS_M, NS_K, device=dev, generator=g)
+    x = torch.where(torch.rand(NS_M, NS_K, device=dev, generator=g) < 0.001, x * 20, x).to(torch.bfloat16)
+    w = (torch.randn(NS_N, NS_K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn(NS_N, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+    qw, sw = ops.quantize_rows_fp8(w)
+    del w
+    qx, sx = ops.quantize_rows_fp8(x)
+
+    ms_linear = time_loop(lambda: ops.linear_fp8(x, qw, sw, bias, 1), args.steps, args.warmup)
+    ms_gemm = time_loop(lambda: ops.gemm_fp8_rowcol(qx, qw, sx, sw, bias, 1), args.steps, args.warmup)
+    ms_quant = time_loop(lambda: ops.quantize_rows_fp8(x), args.steps, args.warmup)
+    f_ns = gemm_flops(NS_M, NS_K, NS_N)
+    linear_tflops = f_ns / (ms_linear * 1e-3) / 1e12
+    gemm_tflops = f_ns / (ms_gemm * 1e-3) / 1e12
+    quant_bytes = NS_M * NS_K * 3 + NS_M * 4
+    log(f"north-star linear {ms_linear:.3f} ms ({linear_tflops:.0f} TFLOP/s); "
+        f"GEMM {ms_gemm:.3f} ms ({gemm_tflops:.0f} TFLOP/s); act quant {ms_quant * 1e3:.1f} us")
+    del x, qx
+
+    # ---------------- config 1 linear
+    x1 = torch.randn(C1_M, C1_K, device=dev, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(C1_N, C1_K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    b1 = (torch.randn(C1_N, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+    qw1, sw1 = ops.quantize_rows_fp8(w1)
+    ms_c1 = time_loop(lambda: ops.linear_fp8(x1, qw1, sw1, b1, 0), args.steps, args.warmup)
+    c1_tflops = gemm_flops(C1_M, C1_K, C1_N) / (ms_c1 * 1e-3) / 1e12
+    log(f"config-1 linear {ms_c1 * 1e3:.1f} us ({c1_tflops:.0f} TFLOP/s)")
+    del x1, w1
+
+    # ---------------- config 2: KV quantize-on-write
+    gain = torch.empty(KV_H, device=dev).uniform_(0.5, 4.0, generator=g)
+    k = (torch.randn(1, KV_H, KV_L, KV_D, device=dev, generator=g) * gain[None, :, None, None]).to(torch.bfloat16)
+    v = (torch.randn(1, KV_H, KV_L, KV_D, device=dev, generator=g) * gain[None, :, None, None]).to(torch.bfloat16)
+    cache = kvc.make_fp8_kv_block(1, ATT_CHUNKS * KV_L, KV_H, KV_D, device=dev)
+    kt, vt = k.transpose(1, 2), v.transpose(1, 2)        # [1, L, H, D] views of BHSD data
+    slot = (ATT_CHUNKS - 1) * KV_L
+    kv_fn = lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"], cache["v_scale"], kt, vt, slot)
+    ms_kv = time_loop(kv_fn, args.steps, args.warmup)
+    kv_gbs = kv_write_bytes() / (ms_kv * 1e-3) / 1e9
+    log(f"KV write {ms_kv * 1e3:.1f} us ({kv_gbs:.0f} GB/s)")
+
+    # ---------------- config 3: chunk attention over 8 chunks
+    for c in range(ATT_CHUNKS):
+        gain = torch.empty(KV_H, device=dev).uniform_(0.5, 4.0, generator=g)
+        kc = (torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        vc = (torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        kvc.quantize_kv_pair_into(cache, kc, vc, c * KV_L)
+    del kc, vc, k, v
+    q = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+    lk = ATT_CHUNKS * KV_L
+    att_fn = lambda: ca.chunk_attention(q, cache, lk, q_pos0=(ATT_CHUNKS - 1) * KV_L, chunk_len=KV_L)
+    ms_att = time_loop(att_fn, max(2, args.steps // 4), max(1, args.warmup // 2))
+    att_tflops = attn_flops(KV_H, KV_L, lk, KV_D) / (ms_att * 1e-3) / 1e12
+    att_gbs = attn_unique_bytes(KV_H, KV_L, lk, KV_D) / (ms_att * 1e-3) / 1e9
+    log(f"chunk attention {ms_att:.3f} ms ({att_tflops:.0f} TFLOP/s, {att_gbs:.0f} GB/s unique)")
+    # decode-style variant: 128 queries over the same cache (HBM-bound regime)
+    qd = q[:, :128].contiguous()
+    ms_dec = time_loop(lambda: ca.chunk_attention(qd, cache, lk), args.steps, args.warmup)
+    dec_gbs = attn_unique_bytes(KV_H, 128, lk, KV_D) / (ms_dec * 1e-3) / 1e9
+    log(f"decode-style attention (Lq=128) {ms_dec * 1e3:.1f} us ({dec_gbs:.0f} GB/s)")
+
+    # ---------------- CPU baseline: the oracle's dequantize-then-matmul
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_seconds, log)
+
+    result = {
+        "metric": "FP8 linear TFLOP/s (% MFMA peak); FP8-KV chunk attn ms + HBM GB/s",
+        "value": round(linear_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_linear + ms_kv + ms_att, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "e4m3 (fp32 accumulate); attention bf16 MFMA over e4m3 KV",
+        "data": "synthetic (seeded N(0,1) activations with 0.1% x20 outliers, N(0,0.02) weights)",
+        "config": {
+            "workload": "north-star FP8 linear [10800x3072]x[3072x12288]+bias+GELU; "
+                        "config-2 KV write; config-3 chunk attention (Lq 10800, Lk 86400, H 24, D 128)",
+            "linear_mnk": [NS_M, NS_N, NS_K],
+            "kv_write": [1, KV_H, KV_L, KV_D],
+            "attention": {"Lq": KV_L, "Lk": lk, "H": KV_H, "D": KV_D, "chunk": KV_L},
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(gemm_tflops, 2),
+            "peak": FP8_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
+            "traffic": None,
+        },
+        "linear": {"ms": round(ms_linear, 4), "tflops": round(linear_tflops, 2),
+                   "frac_fp8_peak": round(linear_tflops / FP8_PEAK_TFLOPS, 4),
+                   "gemm_ms": round(ms_gemm, 4), "act_quant_us": round(ms_quant * 1e3, 2),
+                   "act_quant_gbs": round(quant_bytes / (ms_quant * 1e-3) / 1e9, 1)},
+        "config1_linear": {"us": round(ms_c1 * 1e3, 2), "tflops": round(c1_tflops, 2),
+                           "frac_fp8_peak": round(c1_tflops / FP8_PEAK_TFLOPS, 4)},
+        "kv_write": {"us": round(ms_kv * 1e3, 2), "gbs": round(kv_gbs, 1),
+                     "frac_hbm": round(kv_gbs / HBM_PEAK_GBS, 4), "bytes": kv_write_bytes()},
+        "attention": {"ms": round(ms_att, 4), "tflops": round(att_tflops, 2),
+                      "frac_bf16_peak": round(att_tflops / BF16_PEAK_TFLOPS, 4),
+                      "unique_hbm_gbs": round(att_gbs, 1),
+                      "decode_lq128_us": round(ms_dec * 1e3, 2),
+                      "decode_lq128_gbs": round(dec_gbs, 1),
+                      "decode_frac_hbm": round(dec_gbs / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+
+
+def cpu_baseline(seconds, log):
+    """Oracle dequantize-then-matmul of a row sample of the north-star linear on
+    the host's cores: per-token quant in C (1 thread), dequant + float64 BLAS matmul."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+    from oracle import oracle as O
+
+    cores = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    rows = 256
+    x = rng.standard_normal((rows, NS_K)).astype(np.float32)
+    w = (rng.standard_normal((NS_N, NS_K)) * 0.02).astype(np.float32)
+    xb = O.f32_to_bf16_bits(x)
+    qw, sw = O.quantize_rows_fp8(O.f32_to_bf16_bits(w))
+    bias = rng.standard_normal(NS_N) * 0.01
+    with threadpool_limits(limits=cores, user_api="blas"):
+        blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
+        n, t0 = 0, time.perf_counter()
+        while True:
+            qx, sx = O.quantize_rows_fp8(xb)
+            O.linear_reference(qx, sx, qw, sw, bias, gelu=True)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 50:
+                break
+    tflops = gemm_flops(rows, NS_K, NS_N) * n / el / 1e12
+    log(f"cpu baseline {tflops * 1e3:.2f} GFLOP/s over {n} x {rows} rows in {el:.1f} s")
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(blas[0]) if blas else cores,
+            "kind": "port",
+            "sample": f"{n} x {rows} token rows of the north-star linear ({rows}x{NS_K}x{NS_N}): "
+                      f"oracle per-token e4m3 quant (C) + dequantize-then-matmul (numpy float64 BLAS) "
+                      f"+ bias + GELU, {el:.1f} s"}
+
+
+if __name__ == "__main__":
+    main()

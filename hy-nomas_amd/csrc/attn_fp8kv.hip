@@ -1,0 +1,513 @@
+// Block-causal chunk attention over an FP8 (or INT8-compat) KV cache, gfx950.
+//
+//   O = softmax(Q K^T * scale) V,   K, V = code * per-(token, head) scale
+//
+// Work decomposition: one workgroup = 4 waves = 128 queries of one (batch,
+// head); each wave owns 32 queries (one 32-column MFMA block), and two
+// workgroups share a CU (2 waves per SIMD), so one wave's softmax VALU work
+// overlaps the other's MFMAs. Keys stream
+// through LDS in tiles of 64: the cache segment's 1-byte codes are widened to
+// bf16 once per workgroup while they are written to LDS (exact: every e4m3
+// and int8 code is a bf16 value), and the per-token fp32 scales are staged
+// beside them. The scales never touch the bf16 operands: the K scale (times
+// softmax_scale * log2 e) multiplies the fp32 logits and the V scale
+// multiplies the fp32 probabilities before they are packed for the PV MFMA,
+// so K and V enter as code * scale in fp32 -- not rounded to bf16 first. The
+// optional unquantized tail (the current chunk's bf16 K/V) is copied into the
+// same LDS format with unit scales, so one compute path serves both segments.
+//
+// Per tile the wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: the
+// MFMA output puts one query per lane column, so the online-softmax max/sum
+// are lane-local plus one exchange with lane ^ 32. P^T is packed to bf16 in
+// registers and reused as the B operand of O^T += V^T P^T (V^T is transposed
+// into LDS with a key order that matches the S^T register layout). Two LDS
+// stages: the next tile's global loads are in flight in registers while the
+// MFMAs consume the current one.
+//
+// Mask: key position p is visible to query position r iff p / chunk <= r / chunk
+// (chunk <= 0: all visible). Tiles wholly beyond the last query's chunk are
+// never visited; tiles wholly visible to every query of the workgroup skip
+// the per-element test.
+#include "hn_capi_internal.h"
+#include "hn_common.h"
+
+namespace hn {
+namespace attn {
+
+constexpr int D = 128;
+constexpr int BKV = 64;            // keys per tile
+constexpr int NW = 4;              // waves per workgroup
+constexpr int NT = 64 * NW;
+constexpr int QW = 32;             // queries per wave
+constexpr int BQ = QW * NW;        // queries per workgroup
+constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
+constexpr int VROW = BKV * 2 + 16; // V^T tile row: 64 bf16 + 16 B pad
+constexpr int K_BYTES = BKV * KROW;
+constexpr int V_BYTES = D * VROW;
+constexpr int S_BYTES = 2 * BKV * 4;  // per-key K and V scales (fp32)
+constexpr int STAGE = K_BYTES + V_BYTES + S_BYTES;
+
+struct Params {
+    const uint16_t* q;
+    const uint8_t* kc;
+    const uint8_t* vc;
+    const float* ks;
+    const float* vs;
+    const uint16_t* kcur;
+    const uint16_t* vcur;
+    uint16_t* out;
+    int64_t qs0, qs1, qs2;
+    int64_t cs0, cs1, cs2;
+    int64_t ss0, ss1, ss2;
+    int64_t us0, us1, us2;
+    int64_t os0, os1, os2;
+    int64_t Lq, H, kv_len, cur_len, q_pos0, chunk;
+    float scale_log2;  // softmax_scale * log2(e)
+    int fmt;
+    int q_tiles;       // ceil(Lq / BQ)
+    int work;          // B * H * q_tiles
+    int per_xcd;       // ceil(work / 8)
+};
+
+// Position of key j (0..63) of a tile inside a V^T row: within each 16-key
+// slice, bits 2 and 3 of the index are swapped. Slice t of the tile is then
+// laid out so that lane half h's eight k-slots of the PV MFMA are keys
+// {16t + 4h + 0..3, 16t + 8 + 4h + 0..3}, exactly the keys that lane holds
+// in S^T registers 8t' .. 8t'+7 (see compute_tile).
+HN_DEVICE int vpos(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+
+// Two codes (bytes 2 hi, 2 hi + 1 of w) -> their two exact bf16 values. The
+// gfx950 conversion is used with a unit scale only: its scale operand applies
+// just the exponent of the fp32 value, so per-token scales are applied in fp32
+// by the caller instead.
+HN_DEVICE uint32_t cvt2(uint32_t w, bool hi, int fmt) {
+    if (fmt == HN_KV_FP8) {
+        bf16x2 r = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
+                      : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    const uint32_t sh = hi ? 16 : 0;
+    const float a = (float)(int8_t)((w >> sh) & 0xffu);
+    const float b = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
+    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+}
+
+// 16 codes (one uint4) -> 16 bf16 as 8 dwords.
+HN_DEVICE void cvt16(const uint4& c, int fmt, uint32_t (&o)[8]) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o[2 * i] = cvt2(w[i], false, fmt);
+        o[2 * i + 1] = cvt2(w[i], true, fmt);
+    }
+}
+
+// Registers holding one cache tile between its global load and its LDS
+// write (the load is issued before the tile in LDS is consumed).
+// K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
+// V: thread t owns keys 2 (t / 8), +1 and 16 dims at 16 (t % 8).
+struct CacheRegs {
+    uint4 k[2];
+    uint4 v[2];
+    float sk[2], sv[2];
+};
+
+HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t h,
+                               int64_t first, int64_t count) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int u = t + NT * i;
+        int64_t j = u >> 3;
+        j = j < count ? j : count - 1;  // clamp inside the segment; masked later
+        const int64_t tok = first + j;
+        r.k[i] = *reinterpret_cast<const uint4*>(p.kc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (u & 7) * 16);
+        r.sk[i] = p.ks[b * p.ss0 + tok * p.ss1 + h * p.ss2];
+    }
+    const int kp = t >> 3, dg = t & 7;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int64_t j = kp * 2 + i;
+        j = j < count ? j : count - 1;
+        const int64_t tok = first + j;
+        r.v[i] = *reinterpret_cast<const uint4*>(p.vc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + dg * 16);
+        r.sv[i] = p.vs[b * p.ss0 + tok * p.ss1 + h * p.ss2];
+    }
+}
+
+// V^T write of 2 consecutive keys x 16 dims: cv[key][e] holds dims (2e, 2e+1).
+HN_DEVICE void store_vt(uint8_t* vl, const uint32_t (&cv)[2][8]) {
+    const int t = threadIdx.x;
+    const int kp = t >> 3, dg = t & 7;
+    const int pos = vpos(kp * 2);  // the pair stays adjacent: vpos keeps bits 0-1
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = __builtin_amdgcn_perm(cv[1][e], cv[0][e], 0x05040100u);  // dim 2e
+        const uint32_t hi = __builtin_amdgcn_perm(cv[1][e], cv[0][e], 0x07060302u);  // dim 2e+1
+        const int d0 = dg * 16 + 2 * e;
+        *reinterpret_cast<uint32_t*>(vl + d0 * VROW + pos * 2) = lo;
+        *reinterpret_cast<uint32_t*>(vl + (d0 + 1) * VROW + pos * 2) = hi;
+    }
+}
+
+// Per-key scales in LDS: [0, 64) K scale * softmax_scale * log2 e, [64, 128) V scale.
+HN_DEVICE float* stage_scales(uint8_t* st) { return reinterpret_cast<float*>(st + K_BYTES + V_BYTES); }
+
+HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st) {
+    const int t = threadIdx.x;
+    float* sc = stage_scales(st);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int u = t + NT * i;
+        uint32_t o[8];
+        cvt16(r.k[i], p.fmt, o);
+        uint4* dst = reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32);
+        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        if ((u & 7) == 0) sc[u >> 3] = r.sk[i] * p.scale_log2;
+    }
+    uint32_t cv[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) cvt16(r.v[i], p.fmt, cv[i]);
+    store_vt(st + K_BYTES, cv);
+    if ((t & 7) == 0) {
+        sc[BKV + (t >> 3) * 2] = r.sv[0];
+        sc[BKV + (t >> 3) * 2 + 1] = r.sv[1];
+    }
+}
+
+// Unquantized tail tile (bf16 K/V of the current chunk): load and write to LDS
+// in one go (not prefetched: it is at most one chunk of the keys).
+HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t first,
+                              int64_t count, uint8_t* st) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int u = t + NT * i;
+        int64_t j = u >> 3;
+        j = j < count ? j : count - 1;
+        const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (u & 7) * 16;
+        const uint4 lo = *reinterpret_cast<const uint4*>(src);
+        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
+        uint4* dst = reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32);
+        dst[0] = lo;
+        dst[1] = hi;
+    }
+    const int kp = t >> 3, dg = t & 7;
+    uint32_t cv[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        int64_t j = kp * 2 + i;
+        j = j < count ? j : count - 1;
+        const uint16_t* src = p.vcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + dg * 16;
+        const uint4 lo = *reinterpret_cast<const uint4*>(src);
+        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
+        cv[i][0] = lo.x; cv[i][1] = lo.y; cv[i][2] = lo.z; cv[i][3] = lo.w;
+        cv[i][4] = hi.x; cv[i][5] = hi.y; cv[i][6] = hi.z; cv[i][7] = hi.w;
+    }
+    store_vt(st + K_BYTES, cv);
+    float* sc = stage_scales(st);
+    if (t < BKV) sc[t] = p.scale_log2;
+    else if (t < 2 * BKV) sc[t] = 1.0f;
+}
+
+HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+HN_DEVICE bf16x8 ld_bf16x8(const uint8_t* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+__global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+    // XCD-aware work order: workgroup ids are dealt round-robin to the 8 XCDs,
+    // so id % 8 picks a contiguous range of work items -- the query tiles of
+    // the same few heads share that XCD's L2 while they stream its K/V.
+    const int id = blockIdx.x;
+    const int w = (id & 7) * p.per_xcd + (id >> 3);
+    if (w >= p.work) return;
+    const int qt = w % p.q_tiles;
+    const int64_t h = (w / p.q_tiles) % p.H;
+    const int64_t b = w / (p.q_tiles * (int)p.H);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int64_t row = (int64_t)qt * BQ + wave * QW + col;  // this lane's query row
+    const bool qvalid = row < p.Lq;
+    const int64_t qrow = qvalid ? row : p.Lq - 1;
+    const int64_t qpos = p.q_pos0 + qrow;
+
+    // Q^T fragments (B operand): query column `col`, dims 16 s + 8 half .. +8
+    // for K slice s (the K fragments use the same dim mapping).
+    bf16x8 qf[8];
+    {
+        const uint16_t* src = p.q + b * p.qs0 + qrow * p.qs1 + h * p.qs2 + half * 8;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl)
+            qf[sl] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(src + 16 * sl));
+    }
+
+    // Visible key range for this workgroup (positions): up to the end of the
+    // last query's chunk.
+    const int64_t wg_first_q = (int64_t)qt * BQ;
+    int64_t wg_last_q = wg_first_q + BQ - 1;
+    wg_last_q = wg_last_q < p.Lq - 1 ? wg_last_q : p.Lq - 1;
+    const int64_t r_first = p.q_pos0 + wg_first_q, r_last = p.q_pos0 + wg_last_q;
+    int64_t pos_end = p.kv_len + p.cur_len;
+    if (p.chunk > 0) {
+        const int64_t lim = (r_last / p.chunk + 1) * p.chunk;
+        pos_end = pos_end < lim ? pos_end : lim;
+    }
+    const int64_t cache_end = p.kv_len < pos_end ? p.kv_len : pos_end;
+    const int64_t tail_end = pos_end - p.kv_len;  // tail keys visited (may be <= 0)
+    const int n_cache = (int)((cache_end + BKV - 1) / BKV);
+    const int n_tail = tail_end > 0 ? (int)((tail_end + BKV - 1) / BKV) : 0;
+    const int n_tiles = n_cache + n_tail;
+    const int64_t qchunk = p.chunk > 0 ? qpos / p.chunk : 0;
+
+    f32x16 o[4];  // O^T: [dim block], column = this lane's query
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
+    float mrow = -INFINITY;
+    float lsum = 0.0f;
+
+    CacheRegs regs;
+    auto tile_geom = [&](int t, bool& cache_seg, int64_t& first, int64_t& count, int64_t& pos0) {
+        if (t < n_cache) {
+            cache_seg = true;
+            first = (int64_t)t * BKV;
+            count = cache_end - first;
+            pos0 = first;
+        } else {
+            cache_seg = false;
+            first = (int64_t)(t - n_cache) * BKV;
+            count = tail_end - first;
+            pos0 = p.kv_len + first;
+        }
+        count = count < BKV ? count : BKV;
+    };
+
+    if (n_tiles > 0) {
+        bool cs;
+        int64_t first, count, pos0;
+        tile_geom(0, cs, first, count, pos0);
+        if (cs) {
+            load_cache_tile(p, regs, b, h, first, count);
+            store_cache_tile(p, regs, smem);
+        } else {
+            copy_tail_tile(p, b, h, first, count, smem);
+        }
+    }
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const uint8_t* st = smem + (t & 1) * STAGE;
+        bool cs;
+        int64_t first, count, pos0;
+        tile_geom(t, cs, first, count, pos0);
+        bool ncs = false;
+        int64_t nf = 0, nc = 0, np = 0;
+        if (t + 1 < n_tiles) {
+            tile_geom(t + 1, ncs, nf, nc, np);
+            if (ncs) load_cache_tile(p, regs, b, h, nf, nc);
+        }
+
+        // ---- S^T = K Q^T: two 32-key blocks x this wave's 32 queries
+        f32x16 sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.0f;
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x8 kf = ld_bf16x8(st + (kb * 32 + col) * KROW + (16 * sl + 8 * half) * 2);
+                sacc[kb] = mfma_bf16(kf, qf[sl], sacc[kb]);
+            }
+
+        // ---- mask: keys past the segment end, and the chunk-causal rule.
+        // Register v of block kb holds key 32 kb + 8 (v/4) + 4 half + v%4.
+        const int64_t last_pos = pos0 + count - 1;
+        const bool full = count == BKV && (p.chunk <= 0 || last_pos / p.chunk <= r_first / p.chunk);
+        if (!full) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    bool vis = j < count;
+                    if (p.chunk > 0) vis = vis && ((pos0 + j) / p.chunk <= qchunk);
+                    if (!vis) sacc[kb][v] = -INFINITY;
+                }
+        }
+
+        // ---- logits in log2 units: t = s * (k_scale * softmax_scale * log2 e).
+        // Register v of block kb holds key 32 kb + 8 (v/4) + 4 half + v%4, so
+        // each group of 4 registers takes 4 consecutive scales (one 16-byte read).
+        const float* sc = reinterpret_cast<const float*>(st + K_BYTES + V_BYTES);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float4 ks4 = *reinterpret_cast<const float4*>(sc + kb * 32 + 8 * g4 + 4 * half);
+                sacc[kb][4 * g4 + 0] *= ks4.x;
+                sacc[kb][4 * g4 + 1] *= ks4.y;
+                sacc[kb][4 * g4 + 2] *= ks4.z;
+                sacc[kb][4 * g4 + 3] *= ks4.w;
+            }
+
+        // ---- online softmax for this lane's query (keys split over lane ^ 32)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[kb][v]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mrow, mx);
+        const float muse = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(mrow - muse);
+        mrow = mnew;
+        float rs = 0.0f;
+        bf16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb, times the V scale
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const float4 va = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 4 * half);
+                const float4 vb = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 8 + 4 * half);
+                const float vsc[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+                bf16x8 x;
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) {
+                    const float pv = __builtin_amdgcn_exp2f(sacc[kb][8 * tt + e2] - muse);
+                    rs += pv;
+                    x[e2] = (__bf16)(pv * vsc[e2]);
+                }
+                pf[kb][tt] = x;
+            }
+        rs += __shfl_xor(rs, 32, 64);
+        lsum = lsum * alpha + rs;
+        // Rescale O only when some lane's running max moved (wave-uniform test).
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+        }
+
+        // ---- O^T += V^T P^T over the four 16-key slices of the tile
+        const uint8_t* vl = st + K_BYTES;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int slice = kb * 2 + tt;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const bf16x8 vf = ld_bf16x8(vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2);
+                    o[db] = mfma_bf16(vf, pf[kb][tt], o[db]);
+                }
+            }
+
+        if (t + 1 < n_tiles) {
+            uint8_t* nst = smem + ((t + 1) & 1) * STAGE;
+            if (ncs) store_cache_tile(p, regs, nst);
+            else copy_tail_tile(p, b, h, nf, nc, nst);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: O = O^T / l; the lane holds dims 32 db + 8 (v/4) + 4 half + v%4
+    if (qvalid) {
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        uint16_t* dst = p.out + b * p.os0 + row * p.os1 + h * p.os2;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int d = db * 32 + vq * 8 + half * 4;
+                const uint32_t w0 = f32_to_bf16_bits(o[db][vq * 4] * inv) |
+                                    (f32_to_bf16_bits(o[db][vq * 4 + 1] * inv) << 16);
+                const uint32_t w1 = f32_to_bf16_bits(o[db][vq * 4 + 2] * inv) |
+                                    (f32_to_bf16_bits(o[db][vq * 4 + 3] * inv) << 16);
+                *reinterpret_cast<uint2*>(dst + d) = make_uint2(w0, w1);
+            }
+    }
+}
+
+}  // namespace attn
+}  // namespace hn
+
+using namespace hn;
+
+extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
+                             int64_t H, int64_t D, const void* kc, const void* vc,
+                             const int64_t* cs, const float* ks, const float* vs,
+                             const int64_t* ss, int64_t kv_len, const void* kcur,
+                             const void* vcur, const int64_t* curs, int64_t cur_len,
+                             int64_t q_pos0, int64_t chunk_len, float softmax_scale, void* out,
+                             const int64_t* os, void* stream) {
+    HN_REQUIRE(fmt == HN_KV_FP8 || fmt == HN_KV_INT8, HN_E_ARG, "hn_attn_fp8kv: unknown KV format");
+    HN_REQUIRE(D == attn::D, HN_E_ARG, "hn_attn_fp8kv: head dim must be 128");
+    HN_REQUIRE(B >= 0 && Lq >= 0 && H > 0 && kv_len >= 0 && cur_len >= 0 && q_pos0 >= 0, HN_E_ARG,
+               "hn_attn_fp8kv: invalid shape");
+    HN_REQUIRE(qs && os && (kv_len == 0 || (cs && ss)) && (cur_len == 0 || curs), HN_E_ARG,
+               "hn_attn_fp8kv: null stride array");
+    HN_REQUIRE(qs[3] == 1 && os[3] == 1, HN_E_ARG, "hn_attn_fp8kv: head dim must be contiguous");
+    HN_REQUIRE(qs[0] % 8 == 0 && qs[1] % 8 == 0 && qs[2] % 8 == 0 && os[0] % 4 == 0 &&
+                   os[1] % 4 == 0 && os[2] % 4 == 0,
+               HN_E_ARG, "hn_attn_fp8kv: q/out strides misaligned");
+    HN_REQUIRE(aligned(q, 16) && aligned(out, 8), HN_E_ARG, "hn_attn_fp8kv: q/out misaligned");
+    if (kv_len > 0) {
+        HN_REQUIRE(kc && vc && ks && vs, HN_E_ARG, "hn_attn_fp8kv: null cache pointer");
+        HN_REQUIRE(cs[3] == 1 && cs[0] % 16 == 0 && cs[1] % 16 == 0 && cs[2] % 16 == 0, HN_E_ARG,
+                   "hn_attn_fp8kv: cache strides must be multiples of 16 bytes");
+        HN_REQUIRE(aligned(kc, 16) && aligned(vc, 16), HN_E_ARG, "hn_attn_fp8kv: cache misaligned");
+    }
+    if (cur_len > 0) {
+        HN_REQUIRE(kcur && vcur, HN_E_ARG, "hn_attn_fp8kv: null tail pointer");
+        HN_REQUIRE(curs[3] == 1 && curs[0] % 8 == 0 && curs[1] % 8 == 0 && curs[2] % 8 == 0,
+                   HN_E_ARG, "hn_attn_fp8kv: tail strides must be multiples of 8");
+        HN_REQUIRE(aligned(kcur, 16) && aligned(vcur, 16), HN_E_ARG, "hn_attn_fp8kv: tail misaligned");
+    }
+    if (B == 0 || Lq == 0) return HN_OK;
+    HN_REQUIRE(out && q, HN_E_ARG, "hn_attn_fp8kv: null q/out");
+    attn::Params p;
+    p.q = (const uint16_t*)q;
+    p.kc = (const uint8_t*)kc; p.vc = (const uint8_t*)vc;
+    p.ks = ks; p.vs = vs;
+    p.kcur = (const uint16_t*)kcur; p.vcur = (const uint16_t*)vcur;
+    p.out = (uint16_t*)out;
+    p.qs0 = qs[0]; p.qs1 = qs[1]; p.qs2 = qs[2];
+    if (kv_len > 0) {
+        p.cs0 = cs[0]; p.cs1 = cs[1]; p.cs2 = cs[2];
+        p.ss0 = ss[0]; p.ss1 = ss[1]; p.ss2 = ss[2];
+    } else {
+        p.cs0 = p.cs1 = p.cs2 = p.ss0 = p.ss1 = p.ss2 = 0;
+    }
+    if (cur_len > 0) {
+        p.us0 = curs[0]; p.us1 = curs[1]; p.us2 = curs[2];
+    } else {
+        p.us0 = p.us1 = p.us2 = 0;
+    }
+    p.os0 = os[0]; p.os1 = os[1]; p.os2 = os[2];
+    p.Lq = Lq; p.H = H; p.kv_len = kv_len; p.cur_len = cur_len;
+    p.q_pos0 = q_pos0; p.chunk = chunk_len;
+    p.scale_log2 = softmax_scale * 1.4426950408889634f;
+    p.fmt = fmt;
+    const int64_t qt = (Lq + attn::BQ - 1) / attn::BQ;
+    const int64_t work = B * H * qt;
+    HN_REQUIRE(work <= 0x3fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too much work for one launch");
+    p.q_tiles = (int)qt;
+    p.work = (int)work;
+    p.per_xcd = (int)((work + 7) / 8);
+    const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
+    attn::attn_fp8kv_kernel<<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
+    return check_launch("hn_attn_fp8kv");
+}

@@ -1,0 +1,304 @@
+// FP8 (OCP e4m3) GEMM for gfx950 with fp32 accumulation on the CDNA4
+// f8f6f4 matrix cores (v_mfma_f32_32x32x64_f8f6f4).
+//
+//   out[m, n] = epilogue( sum_k a[m, k] * b[n, k] )
+//
+// a: activations [M, K] and b: weights [N, K], both K-contiguous e4m3 (the
+// nn.Linear weight layout). Two scale modes share one mainloop:
+//   ROWCOL    per-token x per-output-channel scales, bias and optional
+//             GELU-tanh fused in the epilogue;
+//   BLOCKWISE 128x128 block scales on both operands (the decoder contract):
+//             each 128-wide K step is promoted into the accumulator with its
+//             own sa * sb factor.
+//
+// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a 256 x 256 output
+// tile; each wave owns 128 x 128 = 4 x 4 MFMA blocks of 32 x 32 (256 fp32
+// accumulators per lane). K advances 128 bytes per step through two LDS
+// stages (2 x 64 KB of the 160 KB per CU): while the MFMAs consume stage s,
+// the next K step's global loads are in flight and land in stage s^1.
+// Rows are 128 bytes in LDS with their eight 16-byte chunks XOR-swizzled by
+// (row & 7), so the 16-byte fragment reads of eight consecutive rows hit
+// eight distinct bank groups.
+//
+// The MFMA's first operand is the weight tile and its second the activation
+// tile, i.e. the wave computes out^T: each lane then holds four consecutive
+// output columns n..n+3 of one row m and stores them as one 8-byte write.
+#include "hn_capi_internal.h"
+#include "hn_common.h"
+
+namespace hn {
+namespace gemm {
+
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int NT = 256;
+constexpr int TILE_BYTES = BM * BK;         // one operand tile, 32 KB
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // A + B
+
+enum Mode { ROWCOL = 0, BLOCKWISE = 1 };
+constexpr int kMaxKT = 256;  // K <= 32768
+
+struct Params {
+    const uint8_t* a;
+    const uint8_t* b;
+    const float* sa;
+    const float* sb;
+    const uint16_t* bias;
+    uint16_t* out;
+    int64_t M, N, K, ldc;
+    int act;
+    int tiles_m, tiles_n;
+};
+
+HN_DEVICE int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
+
+// Direct global -> LDS loads of one operand tile (global_load_lds_dwordx4:
+// 16 bytes per lane, written at M0 + 16 * lane). Each wave fills 8 regions of
+// 1 KB = 8 rows; a lane's bytes land at row lane / 8, physical chunk lane % 8,
+// so the lane fetches the logical chunk (lane % 8) ^ (row & 7) the swizzle
+// puts there. Rows past the operand's end are clamped to its last row: the
+// loads stay in bounds and the rows they fill are never stored.
+//
+// The load is issued from inline asm so the compiler does not track its LDS
+// write: it would otherwise wait for every DMA in flight before any LDS read,
+// serialising the prefetch of stage s^1 behind the MFMAs on stage s. The
+// kernel instead waits explicitly (vmcnt(0) + barrier) at the end of each K
+// step, and its K loop issues no other vector-memory loads.
+HN_DEVICE void dma_16B(const uint8_t* gsrc, uint32_t lds_addr) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(gsrc), "s"(lds_addr)
+        : "memory", "m0");
+}
+
+HN_DEVICE uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+HN_DEVICE void load_tile_lds(uint8_t* lds_tile, const uint8_t* __restrict__ base, int64_t row0,
+                             int64_t rows, int64_t K, int64_t k0, int wave, int lane) {
+    const uint32_t tile_addr = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int rgn = wave * 8 + i;
+        const int r = rgn * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ (lane >> 3);
+        int64_t row = row0 + r;
+        row = row < rows ? row : rows - 1;
+        dma_16B(base + row * K + k0 + (c << 4),
+                __builtin_amdgcn_readfirstlane(tile_addr + rgn * 1024));
+    }
+}
+
+// One 32 x 64 fragment: lane l reads row (l % 32) of the block and the 32
+// bytes [32 (l / 32), +32) of the 64-byte K slice `kh`. A and B use the same
+// lane -> K mapping, so any order of K inside a slice gives the same sum.
+HN_DEVICE i32x8 read_frag(const uint8_t* lds, int row, int kh, int lane) {
+    const int c0 = kh * 4 + (lane >> 5) * 2;
+    const uint4 lo = *reinterpret_cast<const uint4*>(lds + swz(row, c0));
+    const uint4 hi = *reinterpret_cast<const uint4*>(lds + swz(row, c0 + 1));
+    i32x8 f;
+    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+    return f;
+}
+
+HN_DEVICE f32x16 mfma(const i32x8& a, const i32x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+HN_DEVICE float gelu_tanh(float x) {
+    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (e^{2u} + 1)
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    const float t = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
+    return 0.5f * x * (1.0f + t);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE_BYTES];
+    // BLOCKWISE: the wave pair's scale rows, staged once so the K loop needs
+    // no global scale loads: [2 m blocks][KT] then [2 n blocks][KT].
+    __shared__ float sscale[4 * kMaxKT];
+
+    // Tile order: consecutive workgroups walk down M inside a column band of
+    // N so that the weight tile stays hot in L2 across neighbours.
+    const int tile = blockIdx.x;
+    const int tm = tile % p.tiles_m;
+    const int tn = tile / p.tiles_m;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave & 1, wn = wave >> 1;  // wave's 128 x 128 sub-tile
+    const int KT = (int)(p.K / BK);
+
+    if (MODE == BLOCKWISE) {
+        // Blocks wholly past M or N get zero: they are computed, never stored.
+        for (int i = threadIdx.x; i < 4 * KT; i += NT) {
+            const int which = i / KT, kb = i % KT;
+            float v = 0.0f;
+            if (which < 2) {
+                const int64_t mb = (m0 >> 7) + which;
+                if (mb * 128 < p.M) v = p.sa[mb * KT + kb];
+            } else {
+                const int64_t nb = (n0 >> 7) + (which - 2);
+                if (nb * 128 < p.N) v = p.sb[nb * KT + kb];
+            }
+            sscale[i] = v;
+        }
+    }
+
+    f32x16 acc[4][4];  // [n block][m block]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    load_tile_lds(smem, p.a, m0, p.M, p.K, 0, wave, lane);
+    load_tile_lds(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < KT; ++kt) {
+        const uint8_t* cur = smem + (kt & 1) * STAGE_BYTES;
+        if (kt + 1 < KT) {
+            uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE_BYTES;
+            load_tile_lds(nxt, p.a, m0, p.M, p.K, (int64_t)(kt + 1) * BK, wave, lane);
+            load_tile_lds(nxt + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 1) * BK, wave, lane);
+        }
+        const uint8_t* lA = cur;
+        const uint8_t* lB = cur + TILE_BYTES;
+        if (MODE == ROWCOL) {
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                i32x8 fb[4], fa[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) fb[i] = read_frag(lB, wn * 128 + i * 32 + (lane & 31), kh, lane);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) fa[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), kh, lane);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
+            }
+        } else {
+            // Promote this 128-wide K block with its own scale. The wave's
+            // 128 x 128 sub-tile lies inside one 128 x 128 scale block of
+            // each operand, so the factor is uniform over the wave.
+            const float f = sscale[wm * KT + kt] * sscale[(2 + wn) * KT + kt];
+            i32x8 fa0[4], fa1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                fa0[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), 0, lane);
+                fa1[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), 1, lane);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const i32x8 fb0 = read_frag(lB, wn * 128 + i * 32 + (lane & 31), 0, lane);
+                const i32x8 fb1 = read_frag(lB, wn * 128 + i * 32 + (lane & 31), 1, lane);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f32x16 t = {};
+                    t = mfma(fb0, fa0[j], t);
+                    t = mfma(fb1, fa1[j], t);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(t[v], f, acc[i][j][v]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // Epilogue. acc[i][j][v] holds out^T for n = n0 + wn*128 + 32 i + 8 (v/4)
+    // + 4 (lane/32) + v%4 and m = m0 + wm*128 + 32 j + lane%32.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+        if (m >= p.M) continue;
+        const float sam = MODE == ROWCOL ? p.sa[m] : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
+                if (n >= p.N) continue;
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = acc[i][j][vq * 4 + e];
+                if (MODE == ROWCOL) {
+                    const float4 sbn = *reinterpret_cast<const float4*>(p.sb + n);
+                    y[0] *= sam * sbn.x; y[1] *= sam * sbn.y;
+                    y[2] *= sam * sbn.z; y[3] *= sam * sbn.w;
+                    if (p.bias) {
+                        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+                        y[0] += bf16_bits_to_f32(bb.x & 0xffffu);
+                        y[1] += bf16_bits_to_f32(bb.x >> 16);
+                        y[2] += bf16_bits_to_f32(bb.y & 0xffffu);
+                        y[3] += bf16_bits_to_f32(bb.y >> 16);
+                    }
+                    if (p.act == HN_ACT_GELU_TANH) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
+                    }
+                }
+                const uint32_t w0 = f32_to_bf16_bits(y[0]) | (f32_to_bf16_bits(y[1]) << 16);
+                const uint32_t w1 = f32_to_bf16_bits(y[2]) | (f32_to_bf16_bits(y[3]) << 16);
+                *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = make_uint2(w0, w1);
+            }
+        }
+    }
+}
+
+}  // namespace gemm
+}  // namespace hn
+
+using namespace hn;
+
+static int gemm_launch(int mode, const void* a, const void* b, const float* sa, const float* sb,
+                       const void* bias, void* out, int64_t M, int64_t N, int64_t K, int64_t ldc,
+                       int act, void* stream, const char* who) {
+    HN_REQUIRE(M >= 0 && N > 0 && K > 0, HN_E_ARG, "FP8 GEMM: invalid shape");
+    HN_REQUIRE(N % 128 == 0 && K % 128 == 0, HN_E_ARG, "FP8 GEMM: N and K must be multiples of 128");
+    HN_REQUIRE(K <= 128 * gemm::kMaxKT, HN_E_ARG, "FP8 GEMM: K must be <= 32768");
+    HN_REQUIRE(ldc >= N && ldc % 8 == 0, HN_E_ARG, "FP8 GEMM: ldc must be >= N and a multiple of 8");
+    HN_REQUIRE(act == HN_ACT_NONE || act == HN_ACT_GELU_TANH, HN_E_ARG, "FP8 GEMM: unknown activation");
+    HN_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(out, 16) && aligned(sa, 4) &&
+                   aligned(sb, mode == gemm::ROWCOL ? 16 : 4) && aligned(bias, 8),
+               HN_E_ARG, "FP8 GEMM: misaligned pointer");
+    if (M == 0) return HN_OK;
+    HN_REQUIRE(a && b && sa && sb && out, HN_E_ARG, "FP8 GEMM: null pointer");
+    gemm::Params p;
+    p.a = (const uint8_t*)a; p.b = (const uint8_t*)b;
+    p.sa = sa; p.sb = sb;
+    p.bias = (const uint16_t*)bias;
+    p.out = (uint16_t*)out;
+    p.M = M; p.N = N; p.K = K; p.ldc = ldc; p.act = act;
+    const int64_t tm = (M + gemm::BM - 1) / gemm::BM, tn = (N + gemm::BN - 1) / gemm::BN;
+    HN_REQUIRE(tm * tn <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
+    p.tiles_m = (int)tm; p.tiles_n = (int)tn;
+    const dim3 grid((unsigned)(tm * tn));
+    if (mode == gemm::ROWCOL)
+        gemm::gemm_fp8_kernel<gemm::ROWCOL><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+    else
+        gemm::gemm_fp8_kernel<gemm::BLOCKWISE><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+    return check_launch(who);
+}
+
+extern "C" int hn_gemm_fp8_rowcol(const void* a, const void* b, const float* sa, const float* sb,
+                                  const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                                  int64_t ldc, int act, void* stream) {
+    return gemm_launch(gemm::ROWCOL, a, b, sa, sb, bias, out, M, N, K, ldc, act, stream,
+                       "hn_gemm_fp8_rowcol");
+}
+
+extern "C" int hn_gemm_fp8_blockwise(const void* a, const void* b, const float* sa,
+                                     const float* sb, void* out, int64_t M, int64_t N, int64_t K,
+                                     void* stream) {
+    return gemm_launch(gemm::BLOCKWISE, a, b, sa, sb, nullptr, out, M, N, K, N, HN_ACT_NONE,
+                       stream, "hn_gemm_fp8_blockwise");
+}

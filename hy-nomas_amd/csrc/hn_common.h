@@ -1,0 +1,80 @@
+// Device-side helpers shared by the FP8 quantizers, the FP8 GEMM and the
+// FP8-KV chunk attention. gfx950 (CDNA4) only: 64-wide wavefronts, OCP e4m3.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define HN_DEVICE __device__ __forceinline__
+
+namespace hn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+// The e4m3 range used by every scale rule (largest finite OCP e4m3 value).
+constexpr float kE4M3Max = 448.0f;
+
+HN_DEVICE float bf16_bits_to_f32(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+HN_DEVICE uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// fp32 -> OCP e4m3 ("fn") byte, round to nearest even on the e4m3 grid.
+// The grid is extended one step past 448 (480, bit pattern 0x7F): values that
+// round there, values >= 480 and NaN/Inf all give 0x7F | sign, the behaviour of
+// torch's float8_e4m3fn cast that the reference recipes rely on
+// (cutlass_fp8.py:40). Normal range: keep the top 3 mantissa bits and round on
+// the 20 discarded ones; subnormal range (< 2^-6): round a * 2^9 to an integer.
+HN_DEVICE uint32_t e4m3_encode(float f) {
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    uint32_t code;
+    if (a >= 0x43f00000u) {                 // >= 480, Inf, NaN
+        code = 0x7fu;
+    } else if (a < 0x3c800000u) {           // < 2^-6
+        code = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+    } else {
+        const uint32_t keep = a >> 20;      // exponent + 3 mantissa bits
+        const uint32_t rest = a & 0xfffffu; // discarded mantissa bits
+        const uint32_t up = (rest > 0x80000u) | ((rest == 0x80000u) & keep);
+        code = keep - (120u << 3) + up;     // rebias 127 -> 7
+    }
+    return sign | code;
+}
+
+// OCP e4m3 byte -> fp32 (exact).
+HN_DEVICE float e4m3_decode(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    float v;
+    if (e == 0) v = (float)m * 0.001953125f;  // m * 2^-9
+    else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    if (e == 15u && m == 7u) v = __builtin_nanf("");
+    return (c & 0x80u) ? -v : v;
+}
+
+// Max over the `width` lanes of an aligned lane group (width a power of two <= 64).
+template <int WIDTH>
+HN_DEVICE float group_max(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int WIDTH>
+HN_DEVICE float group_sum(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace hn

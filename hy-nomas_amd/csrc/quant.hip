@@ -1,0 +1,374 @@
+// FP8 quantizers for the quantized inference path (gfx950):
+//   * per-row (per-token activations / per-output-channel weights)
+//   * 128x128 blockwise (the decoder GEMM's activation format)
+//   * KV quantize-on-write into a token-major [B, cap, H, D] cache (FP8 and
+//     the INT8-compatible recipe), and KV decode of a valid prefix.
+// All are HBM-bound streaming kernels: 16-byte loads per lane, reductions in
+// registers + cross-lane shuffles, and one IEEE division per element so the
+// codes are bit-identical to the reference's fp32 recipe.
+#include "hn_capi_internal.h"
+#include "hn_common.h"
+
+namespace hn {
+
+// ---------------------------------------------------------------------------
+// Per-row quantization. One 256-thread block per row; each thread keeps up to
+// CPT chunks of 8 bf16 in registers between the amax pass and the encode pass,
+// so the row is read from HBM exactly once.
+template <int CPT>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(
+    const uint16_t* __restrict__ x, int64_t cols, int64_t row_stride, int mode,
+    float amax_floor, uint8_t* __restrict__ q, float* __restrict__ scale) {
+    const int64_t row = blockIdx.x;
+    const uint16_t* xr = x + row * row_stride;
+    const int nchunks = (int)(cols >> 3);
+    uint4 v[CPT];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + i * 256;
+        if (c < nchunks) {
+            v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+            }
+        }
+    }
+    amax = group_max<64>(amax);
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = mode == HN_SCALE_CLAMP ? fmaxf(amax, amax_floor) / kE4M3Max
+                                           : (amax > 0.0f ? amax / kE4M3Max : 1.0f);
+    if (threadIdx.x == 0) scale[row] = s;
+    uint8_t* qr = q + row * cols;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + i * 256;
+        if (c < nchunks) {
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                lo |= e4m3_encode(bf16_bits_to_f32(w[j] & 0xffffu) / s) << (16 * j);
+                lo |= e4m3_encode(bf16_bits_to_f32(w[j] >> 16) / s) << (16 * j + 8);
+                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] & 0xffffu) / s) << (16 * j);
+                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] >> 16) / s) << (16 * j + 8);
+            }
+            *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = make_uint2(lo, hi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 128x128 blockwise quantization: one 256-thread block per (128-row, 128-col)
+// tile; each thread holds 8 chunks of 8 bf16. Rows past `rows` are the zero
+// padding of the reference recipe: they contribute nothing to amax and are
+// not stored.
+__global__ __launch_bounds__(256) void quantize_blockwise_kernel(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, uint8_t* __restrict__ q,
+    float* __restrict__ scale) {
+    const int64_t r0 = (int64_t)blockIdx.x * 128, c0 = (int64_t)blockIdx.y * 128;
+    uint4 v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int id = threadIdx.x + i * 256;
+        const int64_t r = r0 + (id >> 4);
+        const int64_t c = c0 + (id & 15) * 8;
+        if (r < rows) {
+            v[i] = *reinterpret_cast<const uint4*>(x + r * cols + c);
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+            }
+        }
+    }
+    amax = group_max<64>(amax);
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = fmaxf(amax, 1e-4f) / kE4M3Max;
+    if (threadIdx.x == 0) scale[blockIdx.x * gridDim.y + blockIdx.y] = s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int id = threadIdx.x + i * 256;
+        const int64_t r = r0 + (id >> 4);
+        const int64_t c = c0 + (id & 15) * 8;
+        if (r < rows) {
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                lo |= e4m3_encode(bf16_bits_to_f32(w[j] & 0xffffu) / s) << (16 * j);
+                lo |= e4m3_encode(bf16_bits_to_f32(w[j] >> 16) / s) << (16 * j + 8);
+                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] & 0xffffu) / s) << (16 * j);
+                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] >> 16) / s) << (16 * j + 8);
+            }
+            *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(lo, hi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// KV quantize-on-write. A row is one (batch, token, head) vector of D = 128
+// values: 16 lanes x 8 values, so a wave covers 4 rows and a 256-thread block
+// 16 rows. Rows are enumerated head-fastest, which makes consecutive rows
+// consecutive 128-byte code lines of the token-major cache. blockIdx.y selects
+// K (0) or V (1) for the paired launch.
+struct KvArgs {
+    const uint16_t* x[2];
+    uint8_t* q[2];
+    float* s[2];
+    int64_t xs0, xs1, xs2;
+    int64_t qs0, qs1, qs2;
+    int64_t ss0, ss1, ss2;
+    int64_t L, H, rows, start;
+};
+
+HN_DEVICE uint32_t int8_code(float v) {
+    // int8_kv_cache.py:150-157: fp32 round-half-away via floor(v + 0.5) /
+    // ceil(v - 0.5) (each add rounded in fp32), then clamp to +-127.
+    float r = v >= 0.0f ? floorf(v + 0.5f) : ceilf(v - 0.5f);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (uint32_t)(int32_t)r & 0xffu;
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
+    const int sel = blockIdx.y;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (row >= a.rows) return;
+    const int lane16 = threadIdx.x & 15;
+    const int64_t h = row % a.H;
+    const int64_t t = (row / a.H) % a.L;
+    const int64_t b = row / (a.H * a.L);
+    const uint4 v = *reinterpret_cast<const uint4*>(a.x[sel] + b * a.xs0 + t * a.xs1 +
+                                                    h * a.xs2 + lane16 * 8);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
+        f[2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+    amax = group_max<16>(amax);
+    const float qmax = FMT == HN_KV_FP8 ? kE4M3Max : 127.0f;
+    const float s = amax > 0.0f ? amax / qmax : 1.0f;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c0 = FMT == HN_KV_FP8 ? e4m3_encode(f[j] / s) : int8_code(f[j] / s);
+        const uint32_t c1 = FMT == HN_KV_FP8 ? e4m3_encode(f[j + 4] / s) : int8_code(f[j + 4] / s);
+        lo |= c0 << (8 * j);
+        hi |= c1 << (8 * j);
+    }
+    const int64_t tt = t + a.start;
+    *reinterpret_cast<uint2*>(a.q[sel] + b * a.qs0 + tt * a.qs1 + h * a.qs2 + lane16 * 8) =
+        make_uint2(lo, hi);
+    if (lane16 == 0) a.s[sel][b * a.ss0 + tt * a.ss1 + h * a.ss2] = s;
+}
+
+// KV decode of a valid prefix into bf16: y = bf16_rne(decode(q) * s).
+struct KvDecArgs {
+    const uint8_t* q;
+    const float* s;
+    uint16_t* y;
+    int64_t qs0, qs1, qs2;
+    int64_t ss0, ss1, ss2;
+    int64_t ys0, ys1, ys2;
+    int64_t L, H, rows;
+};
+
+template <int FMT>
+__global__ __launch_bounds__(256) void kv_dequantize_kernel(KvDecArgs a) {
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (row >= a.rows) return;
+    const int lane16 = threadIdx.x & 15;
+    const int64_t h = row % a.H;
+    const int64_t t = (row / a.H) % a.L;
+    const int64_t b = row / (a.H * a.L);
+    const uint2 c = *reinterpret_cast<const uint2*>(a.q + b * a.qs0 + t * a.qs1 + h * a.qs2 +
+                                                    lane16 * 8);
+    const float s = a.s[b * a.ss0 + t * a.ss1 + h * a.ss2];
+    const uint32_t cw[2] = {c.x, c.y};
+    uint32_t out[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t word = cw[j >> 1];
+        const uint32_t b0 = (word >> (16 * (j & 1))) & 0xffu;
+        const uint32_t b1 = (word >> (16 * (j & 1) + 8)) & 0xffu;
+        float v0, v1;
+        if (FMT == HN_KV_FP8) {
+            v0 = e4m3_decode(b0);
+            v1 = e4m3_decode(b1);
+        } else {
+            v0 = (float)(int8_t)b0;
+            v1 = (float)(int8_t)b1;
+        }
+        out[j] = f32_to_bf16_bits(v0 * s) | (f32_to_bf16_bits(v1 * s) << 16);
+    }
+    *reinterpret_cast<uint4*>(a.y + b * a.ys0 + t * a.ys1 + h * a.ys2 + lane16 * 8) =
+        make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+}  // namespace hn
+
+using namespace hn;
+
+// ---------------------------------------------------------------------------
+// C ABI
+
+extern "C" int hn_quantize_rows_fp8(const void* x, int64_t rows, int64_t cols,
+                                    int64_t row_stride, int scale_mode, float amax_floor,
+                                    void* q, float* scale, void* stream) {
+    HN_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 16384, HN_E_ARG,
+               "hn_quantize_rows_fp8: cols must be a positive multiple of 8 and <= 16384");
+    HN_REQUIRE(row_stride >= cols && row_stride % 8 == 0, HN_E_ARG,
+               "hn_quantize_rows_fp8: row_stride must be >= cols and a multiple of 8");
+    HN_REQUIRE(scale_mode == HN_SCALE_CLAMP || scale_mode == HN_SCALE_ZERO_ONE, HN_E_ARG,
+               "hn_quantize_rows_fp8: unknown scale mode");
+    HN_REQUIRE(aligned(x, 16) && aligned(q, 8) && aligned(scale, 4), HN_E_ARG,
+               "hn_quantize_rows_fp8: x must be 16-byte and q 8-byte aligned");
+    if (rows == 0) return HN_OK;
+    HN_REQUIRE(x && q && scale, HN_E_ARG, "hn_quantize_rows_fp8: null pointer");
+    HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_quantize_rows_fp8: too many rows");
+    const int chunks_per_thread = (int)((cols / 8 + 255) / 256);
+    const dim3 grid((unsigned)rows);
+    hipStream_t st = (hipStream_t)stream;
+    const uint16_t* xp = (const uint16_t*)x;
+    uint8_t* qp = (uint8_t*)q;
+#define HN_ROWS_CASE(N)                                                                   \
+    case N:                                                                               \
+        quantize_rows_kernel<N><<<grid, 256, 0, st>>>(xp, cols, row_stride, scale_mode,  \
+                                                      amax_floor, qp, scale);             \
+        break;
+    switch (chunks_per_thread) {
+        HN_ROWS_CASE(1)
+        HN_ROWS_CASE(2)
+        HN_ROWS_CASE(3)
+        HN_ROWS_CASE(4)
+        HN_ROWS_CASE(5)
+        HN_ROWS_CASE(6)
+        HN_ROWS_CASE(7)
+        HN_ROWS_CASE(8)
+        default:
+            return fail(HN_E_ARG, "hn_quantize_rows_fp8: unsupported width");
+    }
+#undef HN_ROWS_CASE
+    return check_launch("hn_quantize_rows_fp8");
+}
+
+extern "C" int hn_quantize_blockwise_fp8(const void* x, int64_t rows, int64_t cols, void* q,
+                                         float* scale, void* stream) {
+    HN_REQUIRE(rows >= 0 && cols > 0 && cols % 128 == 0, HN_E_ARG,
+               "hn_quantize_blockwise_fp8: cols must be a positive multiple of 128");
+    HN_REQUIRE(aligned(x, 16) && aligned(q, 8) && aligned(scale, 4), HN_E_ARG,
+               "hn_quantize_blockwise_fp8: misaligned pointer");
+    if (rows == 0) return HN_OK;
+    HN_REQUIRE(x && q && scale, HN_E_ARG, "hn_quantize_blockwise_fp8: null pointer");
+    const dim3 grid((unsigned)((rows + 127) / 128), (unsigned)(cols / 128));
+    quantize_blockwise_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)x, rows, cols, (uint8_t*)q, scale);
+    return check_launch("hn_quantize_blockwise_fp8");
+}
+
+static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_t* xs,
+                            int64_t B, int64_t L, int64_t H, int64_t D, void* const q[2],
+                            const int64_t* qs, float* const s[2], const int64_t* ss,
+                            int64_t start, void* stream, const char* who) {
+    if (fmt != HN_KV_FP8 && fmt != HN_KV_INT8) return fail(HN_E_ARG, "unknown KV format");
+    HN_REQUIRE(D == 128, HN_E_ARG, "KV quantization requires head dim 128");
+    HN_REQUIRE(B >= 0 && L >= 0 && H > 0 && start >= 0, HN_E_ARG, "invalid KV shape");
+    HN_REQUIRE(xs && qs && ss, HN_E_ARG, "null stride array");
+    HN_REQUIRE(xs[3] == 1 && qs[3] == 1, HN_E_ARG, "KV head dim must be contiguous");
+    HN_REQUIRE(xs[0] % 8 == 0 && xs[1] % 8 == 0 && xs[2] % 8 == 0, HN_E_ARG,
+               "KV value strides must be multiples of 8 elements");
+    HN_REQUIRE(qs[0] % 8 == 0 && qs[1] % 8 == 0 && qs[2] % 8 == 0, HN_E_ARG,
+               "KV cache strides must be multiples of 8 bytes");
+    for (int i = 0; i < n; ++i)
+        HN_REQUIRE(aligned(x[i], 16) && aligned(q[i], 8) && aligned(s[i], 4), HN_E_ARG,
+                   "misaligned KV pointer");
+    const int64_t rows = B * L * H;
+    if (rows == 0) return HN_OK;
+    for (int i = 0; i < n; ++i) HN_REQUIRE(x[i] && q[i] && s[i], HN_E_ARG, "null KV pointer");
+    KvArgs a;
+    for (int i = 0; i < 2; ++i) {
+        a.x[i] = (const uint16_t*)x[i < n ? i : 0];
+        a.q[i] = (uint8_t*)q[i < n ? i : 0];
+        a.s[i] = s[i < n ? i : 0];
+    }
+    a.xs0 = xs[0]; a.xs1 = xs[1]; a.xs2 = xs[2];
+    a.qs0 = qs[0]; a.qs1 = qs[1]; a.qs2 = qs[2];
+    a.ss0 = ss[0]; a.ss1 = ss[1]; a.ss2 = ss[2];
+    a.L = L; a.H = H; a.rows = rows; a.start = start;
+    const int64_t blocks = (rows + 15) / 16;
+    HN_REQUIRE(blocks <= 0x7fffffffLL, HN_E_ARG, "KV write too large");
+    const dim3 grid((unsigned)blocks, (unsigned)n);
+    if (fmt == HN_KV_FP8)
+        kv_quantize_kernel<HN_KV_FP8><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    else
+        kv_quantize_kernel<HN_KV_INT8><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    return check_launch(who);
+}
+
+extern "C" int hn_kv_quantize(int fmt, const void* x, const int64_t* xs, int64_t B, int64_t L,
+                              int64_t H, int64_t D, void* q, const int64_t* qs, float* scale,
+                              const int64_t* ss, int64_t start, void* stream) {
+    const void* xx[2] = {x, x};
+    void* qq[2] = {q, q};
+    float* sss[2] = {scale, scale};
+    return kv_quantize_impl(fmt, xx, 1, xs, B, L, H, D, qq, qs, sss, ss, start, stream,
+                            "hn_kv_quantize");
+}
+
+extern "C" int hn_kv_quantize_pair(int fmt, const void* k, const void* v, const int64_t* xs,
+                                   int64_t B, int64_t L, int64_t H, int64_t D, void* qk,
+                                   void* qv, const int64_t* qs, float* sk, float* sv,
+                                   const int64_t* ss, int64_t start, void* stream) {
+    const void* xx[2] = {k, v};
+    void* qq[2] = {qk, qv};
+    float* sss[2] = {sk, sv};
+    return kv_quantize_impl(fmt, xx, 2, xs, B, L, H, D, qq, qs, sss, ss, start, stream,
+                            "hn_kv_quantize_pair");
+}
+
+extern "C" int hn_kv_dequantize(int fmt, const void* q, const int64_t* qs, const float* scale,
+                                const int64_t* ss, int64_t B, int64_t valid_len, int64_t H,
+                                int64_t D, void* y, const int64_t* ys, void* stream) {
+    if (fmt != HN_KV_FP8 && fmt != HN_KV_INT8) return fail(HN_E_ARG, "unknown KV format");
+    HN_REQUIRE(D == 128, HN_E_ARG, "KV decode requires head dim 128");
+    HN_REQUIRE(B >= 0 && valid_len >= 0 && H > 0, HN_E_ARG, "invalid KV decode shape");
+    HN_REQUIRE(qs && ss && ys, HN_E_ARG, "null stride array");
+    HN_REQUIRE(qs[3] == 1 && ys[3] == 1, HN_E_ARG, "KV head dim must be contiguous");
+    HN_REQUIRE(qs[0] % 8 == 0 && qs[1] % 8 == 0 && qs[2] % 8 == 0 && ys[0] % 8 == 0 &&
+                   ys[1] % 8 == 0 && ys[2] % 8 == 0,
+               HN_E_ARG, "KV decode strides must be multiples of 8");
+    HN_REQUIRE(aligned(q, 8) && aligned(y, 16) && aligned(scale, 4), HN_E_ARG,
+               "misaligned KV decode pointer");
+    const int64_t rows = B * valid_len * H;
+    if (rows == 0) return HN_OK;
+    HN_REQUIRE(q && scale && y, HN_E_ARG, "null KV decode pointer");
+    KvDecArgs a;
+    a.q = (const uint8_t*)q; a.s = scale; a.y = (uint16_t*)y;
+    a.qs0 = qs[0]; a.qs1 = qs[1]; a.qs2 = qs[2];
+    a.ss0 = ss[0]; a.ss1 = ss[1]; a.ss2 = ss[2];
+    a.ys0 = ys[0]; a.ys1 = ys[1]; a.ys2 = ys[2];
+    a.L = valid_len; a.H = H; a.rows = rows;
+    const int64_t blocks = (rows + 15) / 16;
+    if (fmt == HN_KV_FP8)
+        kv_dequantize_kernel<HN_KV_FP8><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(a);
+    else
+        kv_dequantize_kernel<HN_KV_INT8><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(a);
+    return check_launch("hn_kv_dequantize");
+}

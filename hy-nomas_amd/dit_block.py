@@ -1,0 +1,156 @@
+"""One DiT block forward with FP8 linears and the FP8 KV cache, and the
+multi-block AR chunk step built from it (BASELINE configs 4 and 5).
+
+Block math follows the reference's inference pre/post functions
+(hymm/models/dit/modules/nomas_compile_prepost.py:14-99) for the image stream:
+adaLN modulation from silu(vec); LayerNorm (eps 1e-6, no affine) + modulate;
+Q/K/V projection (fused into one 3072 -> 9216 FP8 GEMM); per-head RMSNorm
+(fp32, eps 1e-6, weight); interleaved-pair RoPE in fp32 over (t, h, w) with
+axes [16, 56, 56] and theta 256 (posemb_layers.py:191-260,401-453); cached
+attention (FP8 cache history + this chunk's bf16 K/V); out-projection and
+gated residual; LayerNorm + modulate; FFN fc1 with GELU-tanh fused into the
+GEMM epilogue, fc2; gated residual. The AR step follows
+hymm/pipeline/causal_ar.py:2348-2432,2624-2645,2852: N denoising passes
+without cache writes, one cache-write pass, then the valid length advances.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .cache_attention import chunk_attention
+from .dit_fp8_linear import FP8StoredLinear, fp8_linear
+from .fp8_kv_cache import make_fp8_kv_block, quantize_kv_pair_into
+from .metrics import stage
+
+
+def rope_tables(frames: int, height: int, width: int, dims=(16, 56, 56), theta: float = 256.0,
+                t_offset: int = 0, device=None):
+    """cos/sin [frames*height*width, sum(dims)] fp32, interleaved (repeat_interleave(2))."""
+    axes = [torch.arange(n, dtype=torch.float32, device=device) for n in (frames, height, width)]
+    axes[0] = axes[0] + t_offset
+    grid = torch.meshgrid(*axes, indexing="ij")
+    cos, sin = [], []
+    for d, g in zip(dims, grid):
+        freqs = 1.0 / (theta ** (torch.arange(0, d, 2, device=device)[: d // 2].float() / d))
+        ang = torch.outer(g.reshape(-1), freqs)
+        cos.append(ang.cos().repeat_interleave(2, dim=1))
+        sin.append(ang.sin().repeat_interleave(2, dim=1))
+    return torch.cat(cos, dim=1), torch.cat(sin, dim=1)
+
+
+def _rms_norm(x, weight, eps):
+    y = x.float()
+    y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + eps)
+    return y.to(x.dtype) * weight
+
+
+def _rotate_half(x):
+    real, imag = x.float().reshape(*x.shape[:-1], -1, 2).unbind(-1)
+    return torch.stack((-imag, real), dim=-1).flatten(3)
+
+
+def _modulate(x, shift, scale):
+    return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+class FP8DiTBlock(nn.Module):
+    """Image stream of one double-stream block at inference, FP8 linears."""
+
+    def __init__(self, hidden: int = 3072, heads: int = 24, mlp_ratio: int = 4,
+                 qk_eps: float = 1e-6, *, device=None, generator=None):
+        super().__init__()
+        self.hidden, self.heads, self.head_dim = hidden, heads, hidden // heads
+        self.qk_eps = qk_eps
+        kw = dict(device=device, dtype=torch.bfloat16)
+
+        def lin(i, o):
+            m = nn.Linear(i, o, **kw)
+            with torch.no_grad():
+                m.weight.normal_(0.0, 0.02, generator=generator)
+                m.bias.normal_(0.0, 0.02, generator=generator)
+            return m
+
+        self.mod = lin(hidden, 6 * hidden)  # tiny GEMV (M = batch), stays bf16
+        self.qkv = FP8StoredLinear(lin(hidden, 3 * hidden))
+        self.proj = FP8StoredLinear(lin(hidden, hidden))
+        self.fc1 = FP8StoredLinear(lin(hidden, mlp_ratio * hidden))
+        self.fc2 = FP8StoredLinear(lin(mlp_ratio * hidden, hidden))
+        self.q_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
+        self.k_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
+
+    def forward(self, img, vec, cos, sin, kv_cache, cache_valid_len: int,
+                update_cache: bool = False):
+        B, L, C = img.shape
+        H, D = self.heads, self.head_dim
+        with stage("modulation"):
+            parts = F.linear(F.silu(vec), self.mod.weight, self.mod.bias).chunk(6, dim=-1)
+            x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
+        with stage("qkv_fp8"):
+            qkv = fp8_linear(self.qkv, x).view(B, L, 3, H, D)
+        with stage("qk_norm_rope"):
+            q, k, v = qkv.unbind(2)
+            q = _rms_norm(q, self.q_norm, self.qk_eps).to(v.dtype)
+            k = _rms_norm(k, self.k_norm, self.qk_eps).to(v.dtype)
+            c = cos.view(1, L, 1, D)
+            s = sin.view(1, L, 1, D)
+            q = (q.float() * c + _rotate_half(q) * s).type_as(v)
+            k = (k.float() * c + _rotate_half(k) * s).type_as(v)
+            v = v.contiguous()
+        if update_cache:
+            with stage("kv_write_fp8"):
+                quantize_kv_pair_into(kv_cache, k, v, cache_valid_len)
+        with stage("cache_attention"):
+            attn = chunk_attention(q, kv_cache, cache_valid_len, k_cur=k, v_cur=v)
+        with stage("post_fp8"):
+            img = img + fp8_linear(self.proj, attn.reshape(B, L, C)) * parts[2].unsqueeze(1)
+            h = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[3], parts[4])
+            h = fp8_linear(self.fc1, h, gelu=True)
+            h = fp8_linear(self.fc2, h)
+            img = img + h * parts[5].unsqueeze(1)
+        return img
+
+
+class FP8ARModel(nn.Module):
+    """A stack of FP8 blocks with one FP8 KV cache per block, stepped one chunk
+    at a time: ``denoise_steps`` passes without cache writes, then one pass
+    at t = 0 that writes this chunk's K/V, then the valid length advances."""
+
+    def __init__(self, depth: int = 40, hidden: int = 3072, heads: int = 24,
+                 latent_shape=(3, 45, 80), max_chunks: int = 17, *, device=None, seed: int = 0):
+        super().__init__()
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.blocks = nn.ModuleList(
+            FP8DiTBlock(hidden, heads, device=device, generator=g) for _ in range(depth))
+        self.latent_shape = tuple(latent_shape)
+        self.tokens_per_chunk = math.prod(latent_shape)
+        self.capacity = max_chunks * self.tokens_per_chunk
+        self.heads, self.head_dim = heads, hidden // heads
+        self.device = device
+        self.caches = [make_fp8_kv_block(1, self.capacity, heads, self.head_dim, device=device)
+                       for _ in range(depth)]
+        self.cache_valid_len = 0
+        self.frames_done = 0
+
+    @torch.no_grad()
+    def forward_chunk(self, img, vec, update_cache: bool):
+        t, h, w = self.latent_shape
+        cos, sin = rope_tables(t, h, w, t_offset=self.frames_done, device=img.device)
+        for block, cache in zip(self.blocks, self.caches):
+            img = block(img, vec, cos, sin, cache, self.cache_valid_len, update_cache)
+        return img
+
+    @torch.no_grad()
+    def generate_chunk(self, noise, vecs_denoise, vec_write, sigmas):
+        """Euler flow updates over the denoising passes, then the cache write."""
+        x = noise
+        for i, vec in enumerate(vecs_denoise):
+            v_pred = self.forward_chunk(x, vec, update_cache=False)
+            x = x + (sigmas[i + 1] - sigmas[i]) * v_pred
+        self.forward_chunk(x, vec_write, update_cache=True)
+        self.cache_valid_len += self.tokens_per_chunk
+        self.frames_done += self.latent_shape[0]
+        return x

@@ -1,0 +1,92 @@
+"""FP8 stored DiT linear: per-output-channel e4m3 weights, per-token dynamic
+e4m3 activations, one fused HIP GEMM with scales, bias and optional GELU-tanh.
+
+Mirror of the reference's DiT quantized linear,
+hymm/models/dit/modules/int8_stored_bf16_linear.py:46-100, whose W8A16 form
+dequantizes to bf16 and calls F.linear. Here the weight stays FP8 and the
+product runs on the gfx950 FP8 matrix cores:
+
+  * ``quantize_weight(w)``  <- quantize_weight (:46-61): per output channel
+    ``s = max(amax, 1e-4) / 448``, ``q = e4m3_rne(w / s)`` (the clamp rule of
+    cutlass_fp8.py:39 over a 1 x K block).
+  * ``FP8StoredLinear``     <- Int8StoredBF16Linear (:64-94): buffers
+    ``weight_q`` / ``weight_scale``, ``dequant_weight()``, the same BF16 input
+    contract (TypeError otherwise).
+  * ``linear_weight(m)``    <- linear_weight (:97-100) for F.linear call sites.
+  * ``fp8_linear(m, x, act)``: the fused call the FP8 block uses in place of
+    ``F.linear(x, linear_weight(m), b)`` (nomas_compile_prepost.py:45-47,80-87).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib as L
+from . import ops
+
+
+def quantize_weight(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-channel FP8 quantization of a [out_features, in_features] weight."""
+    if weight.ndim != 2 or not weight.is_floating_point():
+        raise TypeError("Expected a floating-point [out_features, in_features] weight")
+    if not torch.isfinite(weight).all():
+        raise ValueError("Cannot quantize a weight containing NaN or Inf")
+    q, s = ops.quantize_rows_fp8(weight.to(torch.bfloat16).contiguous(), L.HN_SCALE_CLAMP, 1e-4)
+    return q, s
+
+
+class FP8StoredLinear(nn.Module):
+    """Stores e4m3 weights and fp32 per-channel scales; computes in FP8."""
+
+    def __init__(self, original: nn.Linear):
+        super().__init__()
+        self.in_features = original.in_features
+        self.out_features = original.out_features
+        if self.in_features % 128 or self.out_features % 128:
+            raise ValueError("FP8 linear needs in/out features divisible by 128")
+        q, s = quantize_weight(original.weight.detach())
+        self.register_buffer("weight_q", q)
+        self.register_buffer("weight_scale", s)
+        self.bias = original.bias
+
+    def dequant_weight(self) -> torch.Tensor:
+        return (self.weight_q.float() * self.weight_scale[:, None]).to(torch.bfloat16)
+
+    def forward(self, x: torch.Tensor, act: int = L.HN_ACT_NONE) -> torch.Tensor:
+        if x.dtype != torch.bfloat16:
+            if (x.device.type == "cuda" and torch.is_autocast_enabled("cuda")
+                    and torch.get_autocast_dtype("cuda") == torch.bfloat16):
+                x = x.to(torch.bfloat16)
+            else:
+                raise TypeError(f"FP8 stored Linear requires BF16 input, got {x.dtype}")
+        bias = None if self.bias is None else self.bias.detach().to(torch.bfloat16)
+        y = ops.linear_fp8(x.reshape(-1, x.shape[-1]), self.weight_q, self.weight_scale, bias, act)
+        return y.reshape(*x.shape[:-1], self.out_features)
+
+
+def linear_weight(module: nn.Module) -> torch.Tensor:
+    if isinstance(module, FP8StoredLinear):
+        return module.dequant_weight()
+    return module.weight
+
+
+def fp8_linear(module: nn.Module, x: torch.Tensor, gelu: bool = False) -> torch.Tensor:
+    """Fused FP8 linear (+ GELU-tanh) for FP8StoredLinear; bf16 F.linear otherwise."""
+    if isinstance(module, FP8StoredLinear):
+        return module(x, L.HN_ACT_GELU_TANH if gelu else L.HN_ACT_NONE)
+    y = F.linear(x, module.weight, module.bias)
+    return F.gelu(y, approximate="tanh") if gelu else y
+
+
+@torch.no_grad()
+def convert_to_fp8(model: nn.Module, predicate=None) -> int:
+    """Replace nn.Linear submodules (optionally filtered) with FP8StoredLinear."""
+    targets = []
+    for name, module in model.named_modules():
+        for child_name, child in module.named_children():
+            if isinstance(child, nn.Linear) and (predicate is None or predicate(f"{name}.{child_name}".lstrip("."), child)):
+                targets.append((module, child_name, child))
+    for parent, child_name, child in targets:
+        setattr(parent, child_name, FP8StoredLinear(child))
+    return len(targets)

@@ -1,0 +1,279 @@
+"""torch.library custom ops over the C ABI of libhynomas_fp8.so.
+
+Each op is opaque to torch.compile (a fake implementation gives shapes only),
+launches on the current stream of the input's device, and raises on CPU
+tensors: the FP8 path has no CPU fallback. The custom-op + register_fake
+pattern is the one the reference uses for its FP8 GEMM
+(hymm/models/vae/pixelumm_decoder/cutlass_fp8.py:47-57).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+
+FP8 = torch.float8_e4m3fn
+
+
+def _gpu(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("hy-nomas_amd FP8 kernels need GPU tensors (there is no CPU path)")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _bytes(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint8) if t.dtype in (FP8, torch.int8) else t
+
+
+# --------------------------------------------------------------------------
+# quantizers
+
+@torch.library.custom_op("hy_nomas_amd::quantize_rows_fp8", mutates_args=())
+def quantize_rows_fp8(x: torch.Tensor, scale_mode: int = L.HN_SCALE_CLAMP,
+                      amax_floor: float = 1e-4) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row e4m3 codes and fp32 scales of a bf16 [..., C] tensor."""
+    _gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("quantize_rows_fp8 expects bf16 input")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    q = torch.empty(x2.shape, dtype=FP8, device=x.device)
+    s = torch.empty((x2.shape[0],), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        L.check(L.load().hn_quantize_rows_fp8(
+            x2.data_ptr(), x2.shape[0], x2.shape[1], x2.stride(0), scale_mode, amax_floor,
+            q.data_ptr(), s.data_ptr(), _stream(x)), "hn_quantize_rows_fp8")
+    return q.view(x.shape), s.view(x.shape[:-1])
+
+
+@quantize_rows_fp8.register_fake
+def _(x, scale_mode=L.HN_SCALE_CLAMP, amax_floor=1e-4):
+    return x.new_empty(x.shape, dtype=FP8), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("hy_nomas_amd::quantize_blockwise_fp8", mutates_args=())
+def quantize_blockwise_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """128x128 blockwise e4m3 codes [M,K] and scales [ceil(M/128), K/128]."""
+    _gpu(x)
+    if x.dtype != torch.bfloat16 or x.ndim != 2:
+        raise TypeError("quantize_blockwise_fp8 expects a bf16 [M, K] matrix")
+    x = x.contiguous()
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=FP8, device=x.device)
+    s = torch.empty(((m + 127) // 128, k // 128), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        L.check(L.load().hn_quantize_blockwise_fp8(x.data_ptr(), m, k, q.data_ptr(), s.data_ptr(),
+                                                   _stream(x)), "hn_quantize_blockwise_fp8")
+    return q, s
+
+
+@quantize_blockwise_fp8.register_fake
+def _(x):
+    m, k = x.shape
+    return (x.new_empty((m, k), dtype=FP8),
+            x.new_empty(((m + 127) // 128, k // 128), dtype=torch.float32))
+
+
+# --------------------------------------------------------------------------
+# GEMMs
+
+@torch.library.custom_op("hy_nomas_amd::gemm_fp8_rowcol", mutates_args=())
+def gemm_fp8_rowcol(a: torch.Tensor, b: torch.Tensor, sa: torch.Tensor, sb: torch.Tensor,
+                    bias: Optional[torch.Tensor] = None, act: int = L.HN_ACT_NONE) -> torch.Tensor:
+    """act(a b^T * sa[m] * sb[n] + bias[n]) in bf16; a e4m3 [M,K], b e4m3 [N,K]."""
+    _gpu(a, b, sa, sb, bias)
+    if a.dtype != FP8 or b.dtype != FP8:
+        raise TypeError("gemm_fp8_rowcol expects e4m3 operands")
+    if sa.dtype != torch.float32 or sb.dtype != torch.float32:
+        raise TypeError("gemm_fp8_rowcol expects fp32 scales")
+    if bias is not None and bias.dtype != torch.bfloat16:
+        raise TypeError("gemm_fp8_rowcol expects a bf16 bias")
+    a = a.contiguous()
+    b = b.contiguous()
+    m, k = a.shape
+    n = b.shape[0]
+    if b.shape[1] != k or sa.numel() != m or sb.numel() != n or (bias is not None and bias.numel() != n):
+        raise ValueError("gemm_fp8_rowcol shape mismatch")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+    with torch.cuda.device(a.device):
+        L.check(L.load().hn_gemm_fp8_rowcol(
+            a.data_ptr(), b.data_ptr(), sa.contiguous().data_ptr(), sb.contiguous().data_ptr(),
+            None if bias is None else bias.contiguous().data_ptr(), out.data_ptr(),
+            m, n, k, n, act, _stream(a)), "hn_gemm_fp8_rowcol")
+    return out
+
+
+@gemm_fp8_rowcol.register_fake
+def _(a, b, sa, sb, bias=None, act=L.HN_ACT_NONE):
+    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("hy_nomas_amd::gemm_fp8_blockwise", mutates_args=())
+def gemm_fp8_blockwise(a: torch.Tensor, b: torch.Tensor, sa: torch.Tensor,
+                       sb: torch.Tensor) -> torch.Tensor:
+    """The reference extension's gemm(a, b, sa, sb) with 128x128 block scales."""
+    _gpu(a, b, sa, sb)
+    for t in (a, b, sa, sb):
+        if not t.is_contiguous():
+            raise RuntimeError("Expected contiguous tensors on one device")
+    if a.dtype != FP8 or b.dtype != FP8:
+        raise RuntimeError("Expected E4M3 FP8 inputs")
+    if sa.dtype != torch.float32 or sb.dtype != torch.float32:
+        raise RuntimeError("Expected FP32 scales")
+    if a.dim() != 2 or b.dim() != 2:
+        raise RuntimeError("Expected matrices")
+    m, k = a.shape
+    n = b.shape[0]
+    if not (m > 0 and n > 0 and k > 0 and b.shape[1] == k and n % 128 == 0 and k % 128 == 0):
+        raise RuntimeError("Invalid GEMM shape")
+    if sa.dim() != 2 or tuple(sa.shape) != ((m + 127) // 128, k // 128):
+        raise RuntimeError("Invalid activation scales")
+    if sb.dim() != 2 or tuple(sb.shape) != (n // 128, k // 128):
+        raise RuntimeError("Invalid weight scales")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+    with torch.cuda.device(a.device):
+        L.check(L.load().hn_gemm_fp8_blockwise(a.data_ptr(), b.data_ptr(), sa.data_ptr(),
+                                               sb.data_ptr(), out.data_ptr(), m, n, k,
+                                               _stream(a)), "hn_gemm_fp8_blockwise")
+    return out
+
+
+@gemm_fp8_blockwise.register_fake
+def _(a, b, sa, sb):
+    return a.new_empty((a.shape[0], b.shape[0]), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("hy_nomas_amd::linear_fp8", mutates_args=())
+def linear_fp8(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+               bias: Optional[torch.Tensor] = None, act: int = L.HN_ACT_NONE) -> torch.Tensor:
+    """Per-token dynamic e4m3 activation quant + per-channel-scaled FP8 GEMM.
+    x bf16 [M, K] -> bf16 [M, N]."""
+    qx, sx = quantize_rows_fp8(x, L.HN_SCALE_CLAMP, 1e-4)
+    return gemm_fp8_rowcol(qx, weight, sx, weight_scale, bias, act)
+
+
+@linear_fp8.register_fake
+def _(x, weight, weight_scale, bias=None, act=L.HN_ACT_NONE):
+    return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.bfloat16)
+
+
+# --------------------------------------------------------------------------
+# KV cache
+
+def _kv_fmt(codes: torch.Tensor) -> int:
+    if codes.dtype == FP8:
+        return L.HN_KV_FP8
+    if codes.dtype == torch.int8:
+        return L.HN_KV_INT8
+    raise TypeError("KV codes must be float8_e4m3fn or int8")
+
+
+@torch.library.custom_op("hy_nomas_amd::kv_quantize_pair_",
+                         mutates_args=("k_codes", "v_codes", "k_scale", "v_scale"))
+def kv_quantize_pair_(k_codes: torch.Tensor, v_codes: torch.Tensor, k_scale: torch.Tensor,
+                      v_scale: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      start: int) -> None:
+    """Quantize bf16 K/V [B,L,H,D] into the caches at token offset ``start``."""
+    _gpu(k_codes, v_codes, k_scale, v_scale, k, v)
+    fmt = _kv_fmt(k_codes)
+    if v_codes.dtype != k_codes.dtype or k.stride() != v.stride():
+        raise ValueError("K/V caches and values must share dtype and layout")
+    if k_codes.stride() != v_codes.stride() or k_scale.stride() != v_scale.stride():
+        raise ValueError("K/V caches must share layout")
+    B, Lt, H, D = k.shape
+    with torch.cuda.device(k.device):
+        L.check(L.load().hn_kv_quantize_pair(
+            fmt, k.data_ptr(), v.data_ptr(), L.strides(k), B, Lt, H, D,
+            k_codes.data_ptr(), v_codes.data_ptr(), L.strides(k_codes),
+            k_scale.data_ptr(), v_scale.data_ptr(), L.strides(k_scale), start, _stream(k)),
+            "hn_kv_quantize_pair")
+
+
+@kv_quantize_pair_.register_fake
+def _(k_codes, v_codes, k_scale, v_scale, k, v, start):
+    return None
+
+
+@torch.library.custom_op("hy_nomas_amd::kv_quantize_", mutates_args=("codes", "scale"))
+def kv_quantize_(codes: torch.Tensor, scale: torch.Tensor, x: torch.Tensor, start: int) -> None:
+    _gpu(codes, scale, x)
+    fmt = _kv_fmt(codes)
+    B, Lt, H, D = x.shape
+    with torch.cuda.device(x.device):
+        L.check(L.load().hn_kv_quantize(
+            fmt, x.data_ptr(), L.strides(x), B, Lt, H, D, codes.data_ptr(), L.strides(codes),
+            scale.data_ptr(), L.strides(scale), start, _stream(x)), "hn_kv_quantize")
+
+
+@kv_quantize_.register_fake
+def _(codes, scale, x, start):
+    return None
+
+
+@torch.library.custom_op("hy_nomas_amd::kv_dequantize", mutates_args=())
+def kv_dequantize(codes: torch.Tensor, scale: torch.Tensor, valid_len: int) -> torch.Tensor:
+    """bf16(code * scale) for tokens [0, valid_len): a new [B, valid_len, H, D] tensor."""
+    _gpu(codes, scale)
+    fmt = _kv_fmt(codes)
+    B, _, H, D = codes.shape
+    y = torch.empty((B, valid_len, H, D), dtype=torch.bfloat16, device=codes.device)
+    if valid_len == 0:
+        return y
+    with torch.cuda.device(codes.device):
+        L.check(L.load().hn_kv_dequantize(
+            fmt, codes.data_ptr(), L.strides(codes), scale.data_ptr(), L.strides(scale),
+            B, valid_len, H, D, y.data_ptr(), L.strides(y), _stream(codes)), "hn_kv_dequantize")
+    return y
+
+
+@kv_dequantize.register_fake
+def _(codes, scale, valid_len):
+    B, _, H, D = codes.shape
+    return codes.new_empty((B, valid_len, H, D), dtype=torch.bfloat16)
+
+
+# --------------------------------------------------------------------------
+# attention
+
+@torch.library.custom_op("hy_nomas_amd::attn_fp8kv", mutates_args=())
+def attn_fp8kv(q: torch.Tensor, k_codes: torch.Tensor, v_codes: torch.Tensor,
+               k_scale: torch.Tensor, v_scale: torch.Tensor, kv_len: int,
+               k_cur: Optional[torch.Tensor] = None, v_cur: Optional[torch.Tensor] = None,
+               q_pos0: int = 0, chunk_len: int = 0,
+               softmax_scale: float = -1.0) -> torch.Tensor:
+    """Chunk attention of q [B,Lq,H,D] over cache tokens [0, kv_len) then the
+    optional bf16 tail k_cur/v_cur [B,Lc,H,D]; see hn_attn_fp8kv for the mask."""
+    _gpu(q, k_codes, v_codes, k_scale, v_scale, k_cur, v_cur)
+    if q.dtype != torch.bfloat16:
+        raise TypeError("attn_fp8kv expects bf16 queries")
+    fmt = _kv_fmt(k_codes)
+    B, Lq, H, D = q.shape
+    if softmax_scale <= 0:
+        softmax_scale = D ** -0.5
+    out = torch.empty((B, Lq, H, D), dtype=torch.bfloat16, device=q.device)
+    cur_len = 0 if k_cur is None else k_cur.shape[1]
+    if cur_len and (v_cur is None or v_cur.shape != k_cur.shape or k_cur.stride() != v_cur.stride()
+                    or k_cur.dtype != torch.bfloat16 or v_cur.dtype != torch.bfloat16):
+        raise ValueError("k_cur/v_cur must be matching bf16 tensors")
+    with torch.cuda.device(q.device):
+        L.check(L.load().hn_attn_fp8kv(
+            fmt, q.data_ptr(), L.strides(q), B, Lq, H, D,
+            k_codes.data_ptr(), v_codes.data_ptr(), L.strides(k_codes),
+            k_scale.data_ptr(), v_scale.data_ptr(), L.strides(k_scale), kv_len,
+            None if not cur_len else k_cur.data_ptr(), None if not cur_len else v_cur.data_ptr(),
+            L.strides(k_cur) if cur_len else None, cur_len, q_pos0, chunk_len,
+            float(softmax_scale), out.data_ptr(), L.strides(out), _stream(q)), "hn_attn_fp8kv")
+    return out
+
+
+@attn_fp8kv.register_fake
+def _(q, k_codes, v_codes, k_scale, v_scale, kv_len, k_cur=None, v_cur=None, q_pos0=0,
+      chunk_len=0, softmax_scale=-1.0):
+    return torch.empty_like(q)

@@ -1,0 +1,156 @@
+/*
+ * hynomas_fp8.h -- C ABI of the MI355X (gfx950) FP8 quantized inference path.
+ *
+ * One shared library, libhynomas_fp8.so, built from hy-nomas_amd/csrc/*.hip.
+ * Every pointer argument is a device pointer unless stated otherwise; sizes
+ * and strides are in elements; `stream` is a hipStream_t (NULL = default
+ * stream). Calls are asynchronous with respect to the host: they enqueue work
+ * on `stream` and return. Each function returns HN_OK (0) or a negative HN_E*
+ * code; hn_last_error() then describes the failure (thread-local). Argument
+ * errors are detected on the host before anything is enqueued, so a failed
+ * call has written nothing.
+ *
+ * Byte formats: bf16 is IEEE bfloat16; e4m3 is OCP FP8 E4M3 ("fn": no
+ * infinities, 0x7F/0xFF NaN, max 448), the format of torch.float8_e4m3fn.
+ *
+ * Each entry point names the reference interface (upstream file:line) whose
+ * work it performs; the Python mirror in hy-nomas_amd/ keeps those interfaces'
+ * names, argument meaning and error behaviour on top of these calls.
+ */
+#ifndef HYNOMAS_FP8_H
+#define HYNOMAS_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HN_OK 0
+#define HN_E_ARG (-1)     /* invalid shape, stride, alignment or mode */
+#define HN_E_LAUNCH (-2)  /* the HIP runtime rejected a launch */
+#define HN_E_DEVICE (-3)  /* no usable gfx950 device */
+
+/* Scale rules for FP8 quantization (amax is the max |x| over the block):
+ *   HN_SCALE_CLAMP:    s = max(amax, amax_floor) / 448
+ *                      (cutlass_fp8.py:39, clamp_min(1e-4) / 448.0)
+ *   HN_SCALE_ZERO_ONE: s = amax > 0 ? amax / 448 : 1
+ *                      (int8_kv_cache.py:44,152 with 448 in place of 127)
+ * Codes are e4m3_rne(x / s) with IEEE-754 binary32 division. */
+#define HN_SCALE_CLAMP 0
+#define HN_SCALE_ZERO_ONE 1
+
+/* KV cache storage formats. */
+#define HN_KV_FP8 0   /* e4m3 codes, s = amax>0 ? amax/448 : 1 */
+#define HN_KV_INT8 1  /* int8 codes bit-exact with int8_kv_cache.py:22-58 */
+
+/* GEMM epilogue activations. */
+#define HN_ACT_NONE 0
+#define HN_ACT_GELU_TANH 1  /* F.gelu(approximate="tanh"), nomas_compile_prepost.py:86 */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *hn_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int hn_abi_version(void);
+
+/* Per-row FP8 quantization of a bf16 matrix: one fp32 scale per row.
+ * x: bf16 [rows, cols] with row stride `row_stride` (elements, >= cols, and
+ *    the row start must be 16-byte aligned); q: e4m3 [rows, cols] contiguous;
+ *    scale: fp32 [rows]. cols % 8 == 0, cols <= 16384.
+ * Replaces the activation quantizer of the FP8 linear custom op,
+ * hymm/models/vae/pixelumm_decoder/cutlass_fp8.py:35-41,49 (its recipe with
+ * 1 x cols blocks: per-token activations, per-output-channel weights), whose
+ * per-token form is the DeepGEMM call site fp8.py:19-21,30. */
+int hn_quantize_rows_fp8(const void *x, int64_t rows, int64_t cols, int64_t row_stride,
+                         int scale_mode, float amax_floor, void *q, float *scale,
+                         void *stream);
+
+/* 128x128 blockwise FP8 quantization, rows zero-padded to a multiple of 128.
+ * x: bf16 [rows, cols] contiguous; q: e4m3 [rows, cols]; scale: fp32
+ * [ceil(rows/128), cols/128]; cols % 128 == 0. Scale rule HN_SCALE_CLAMP with
+ * floor 1e-4.
+ * Replaces quantize_blockwise, cutlass_fp8.py:35-44. */
+int hn_quantize_blockwise_fp8(const void *x, int64_t rows, int64_t cols, void *q,
+                              float *scale, void *stream);
+
+/* KV quantize-on-write of one tensor: values [B, L, H, D] (bf16, strides
+ * xs[4]) are written into the cache q [B, cap, H, D] (strides qs[4], 1-byte
+ * codes) and scale [B, cap, H, 1] (fp32, strides ss[3]) at token offset
+ * `start`. One scale per (batch, token, head) row. D == 128, xs[3] == qs[3]
+ * == 1. The caller guarantees start + L <= cap and finite values (the Python
+ * mirror validates both, int8_kv_cache.py:128-141).
+ * Replaces _quantize_rows / quantize_kv_into, int8_kv_cache.py:22-58,125-158. */
+int hn_kv_quantize(int fmt, const void *x, const int64_t *xs, int64_t B, int64_t L,
+                   int64_t H, int64_t D, void *q, const int64_t *qs, float *scale,
+                   const int64_t *ss, int64_t start, void *stream);
+
+/* K and V of one layer in a single launch (same shapes/strides for both).
+ * Replaces quantize_kv_pair_into, int8_kv_cache.py:161-179 (after its
+ * validation, which the Python mirror performs). */
+int hn_kv_quantize_pair(int fmt, const void *k, const void *v, const int64_t *xs,
+                        int64_t B, int64_t L, int64_t H, int64_t D, void *qk, void *qv,
+                        const int64_t *qs, float *sk, float *sv, const int64_t *ss,
+                        int64_t start, void *stream);
+
+/* KV decode of the valid prefix: y[b,t,h,:] = bf16(decode(q[b,t,h,:]) * s[b,t,h]),
+ * t < valid_len. q strides qs[4], scale strides ss[3], y bf16 strides ys[4];
+ * D == 128 with unit innermost strides.
+ * Replaces _dequantize_rows / dequantize_kv, int8_kv_cache.py:61-89,182-205. */
+int hn_kv_dequantize(int fmt, const void *q, const int64_t *qs, const float *scale,
+                     const int64_t *ss, int64_t B, int64_t valid_len, int64_t H, int64_t D,
+                     void *y, const int64_t *ys, void *stream);
+
+/* Row/column-scaled FP8 GEMM with fused epilogue:
+ *   out[m, n] = act(acc[m, n] * sa[m] * sb[n] + bias[n]),  acc = sum_k a[m,k] b[n,k]
+ * a: e4m3 [M, K] row-major; b: e4m3 [N, K] row-major (the nn.Linear weight
+ * layout); sa: fp32 [M]; sb: fp32 [N]; bias: bf16 [N] or NULL; out: bf16
+ * [M, N] with row stride ldc. fp32 accumulation. K % 128 == 0, N % 128 == 0,
+ * a/b/out 16-byte aligned, ldc % 8 == 0.
+ * Replaces F.linear(x, linear_weight(m), b) of the DiT block
+ * (nomas_compile_prepost.py:45-47,80-87 via int8_stored_bf16_linear.py:82-100)
+ * for FP8 weights, and the DeepGEMM per-token GEMM of fp8.py:27-38. */
+int hn_gemm_fp8_rowcol(const void *a, const void *b, const float *sa, const float *sb,
+                       const void *bias, void *out, int64_t M, int64_t N, int64_t K,
+                       int64_t ldc, int act, void *stream);
+
+/* Blockwise-scaled FP8 GEMM, the `gemm(a, b, sa, sb)` contract of the
+ * reference's native extension:
+ *   out[m, n] = bf16( sum_kb sa[m/128, kb] * sb[n/128, kb] * sum_{k in kb} a[m,k] b[n,k] )
+ * a: e4m3 [M, K]; b: e4m3 [N, K]; sa: fp32 [ceil(M/128), K/128]; sb: fp32
+ * [N/128, K/128]; out: bf16 [M, N] contiguous. N % 128 == 0, K % 128 == 0.
+ * Replaces gemm / pixel_gemm, hymm/models/vae/pixelumm_decoder/csrc/cutlass_fp8.cu:20-57
+ * and reactor/hy_nomas_fp8_sm100.cu:67-107. */
+int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const float *sb,
+                          void *out, int64_t M, int64_t N, int64_t K, void *stream);
+
+/* Attention of one chunk's queries over an FP8 KV cache, block-causal at chunk
+ * granularity, optionally followed by an unquantized bf16 tail (the current
+ * chunk's own K/V during denoising passes).
+ *   q:     bf16 [B, Lq, H, D], strides qs[4] (qs[3] == 1), D == 128
+ *   kc,vc: 1-byte codes [B, cap, H, D], strides cs[4] (cs[3] == 1)
+ *   ks,vs: fp32 scales [B, cap, H, 1], strides ss[3]
+ *   kv_len: cached tokens attended, positions 0 .. kv_len-1
+ *   kcur,vcur: bf16 [B, cur_len, H, D] (strides curs[4]) or NULL with cur_len 0;
+ *          tail token j has position kv_len + j
+ *   q_pos0: position of query row 0; query i has position q_pos0 + i
+ *   chunk_len: key at position p is visible to query at position r iff
+ *          p / chunk_len <= r / chunk_len; chunk_len <= 0 makes every key visible
+ *   out:   bf16 [B, Lq, H, D], strides os[4]
+ * O = softmax(Q K^T * softmax_scale) V with K, V dequantized as code * scale;
+ * query rows that see no key are written as zeros.
+ * Replaces the FP8/INT8-cache branch of causal_attention_with_cache_mp,
+ * hymm/models/dit/nomas_cpt.py:529-531,614-625,771-829 (dequantize_kv, cat,
+ * then Flex/FA3/SDPA), and flex_masked_attention, range_attention.py:212-239. */
+int hn_attn_fp8kv(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t Lq, int64_t H,
+                  int64_t D, const void *kc, const void *vc, const int64_t *cs,
+                  const float *ks, const float *vs, const int64_t *ss, int64_t kv_len,
+                  const void *kcur, const void *vcur, const int64_t *curs, int64_t cur_len,
+                  int64_t q_pos0, int64_t chunk_len, float softmax_scale, void *out,
+                  const int64_t *os, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HYNOMAS_FP8_H */

@@ -1,0 +1,81 @@
+import importlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PKG = "hy-nomas_amd"
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+def pytest_collection_modifyitems(config, items):
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        return
+    skip = pytest.mark.skip(reason="no GPU in this environment")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
+
+
+def pkg_module(name: str = ""):
+    return importlib.import_module(PKG + ("." + name if name else ""))
+
+
+@pytest.fixture(scope="session")
+def O():
+    from oracle import oracle
+    oracle.lib()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def dev():
+    import torch
+    return torch.device("cuda:0")
+
+
+def bf16_bits(t):
+    """Raw bits of a bf16 torch tensor as np.uint16."""
+    import torch
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def u8(t):
+    import torch
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+BF16_HALF_ULP_REL = 2.0 ** -8   # |bf16(x) - x| <= 2^-8 |x|
+
+
+def assert_close_bf16(got, ref, max_abs=2e-2, rel_l2=1e-2, what=""):
+    """The north-star float tolerance versus an fp32/fp64-accumulated reference:
+    rel-L2 <= 1e-2, and elementwise |got - ref| <= max(2e-2, 1.5 * 2^-8 * |ref|).
+    The second term only matters above |ref| ~ 3.4, where the bf16 output's own
+    rounding (half an ulp, up to 2^-8 |ref|) approaches the 2e-2 bar; the 1.5
+    covers fp32 accumulation order on top of it."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    diff = np.abs(got - ref)
+    bound = np.maximum(max_abs, 1.5 * BF16_HALF_ULP_REL * np.abs(ref))
+    worst = float(np.max(diff / bound)) if got.size else 0.0
+    err = float(np.max(diff)) if got.size else 0.0
+    denom = float(np.linalg.norm(ref))
+    rel = float(np.linalg.norm(got - ref) / denom) if denom > 0 else err
+    assert worst <= 1.0 and rel <= rel_l2, (
+        f"{what}: max-abs {err:.3e} (worst/bound {worst:.2f}) rel-L2 {rel:.3e}")
+    return err, rel

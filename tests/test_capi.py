@@ -1,0 +1,132 @@
+"""C ABI and host-side boundary checks that need no GPU: every symbol the
+header declares is exported, argument errors are reported before any launch,
+and the Python mirror validates like the reference."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from conftest import ROOT, pkg_module
+
+HEADER = ROOT / "include" / "hynomas_fp8.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return pkg_module("_lib").load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in {HEADER.name} but not exported"
+    assert set(names) == set(pkg_module("_lib").SIGNATURES), "ctypes table out of sync with header"
+
+
+def test_abi_version(lib):
+    assert lib.hn_abi_version() == 1
+
+
+def _err(lib):
+    return lib.hn_last_error().decode()
+
+
+def test_argument_errors_are_reported_without_a_launch(lib):
+    L = pkg_module("_lib")
+    assert lib.hn_quantize_rows_fp8(None, 4, 7, 7, 0, 1e-4, None, None, None) == -1
+    assert "multiple of 8" in _err(lib)
+    assert lib.hn_quantize_blockwise_fp8(None, 4, 100, None, None, None) == -1
+    assert "multiple of 128" in _err(lib)
+    st = (ctypes.c_int64 * 4)(128, 128, 128, 1)
+    assert lib.hn_kv_quantize(0, None, st, 1, 1, 1, 64, None, st, None, st, 0, None) == -1
+    assert "head dim 128" in _err(lib)
+    assert lib.hn_kv_quantize(7, None, st, 1, 1, 1, 128, None, st, None, st, 0, None) == -1
+    assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 16, 100, 128, 100, 0, None) == -1
+    assert "multiples of 128" in _err(lib)
+    assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 16, 128, 128, 128, 9, None) == -1
+    assert "activation" in _err(lib)
+    assert lib.hn_gemm_fp8_blockwise(None, None, None, None, None, 16, 128, 96, None) == -1
+    assert lib.hn_attn_fp8kv(0, None, st, 1, 1, 1, 64, None, None, st, None, None, st, 0,
+                             None, None, None, 0, 0, 0, 1.0, None, st, None) == -1
+    assert "head dim" in _err(lib)
+    # zero-size work is a no-op that needs no pointers
+    assert lib.hn_quantize_rows_fp8(None, 0, 8, 8, 0, 1e-4, None, None, None) == L.HN_OK
+    assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 0, 128, 128, 128, 0, None) == L.HN_OK
+
+
+def test_ops_refuse_cpu_tensors():
+    ops = pkg_module("ops")
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.quantize_rows_fp8(x)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.linear_fp8(x, torch.zeros(128, 128, dtype=torch.float8_e4m3fn), torch.ones(128))
+
+
+def test_kv_api_validates_before_writing():
+    kvc = pkg_module("fp8_kv_cache")
+    cache = kvc.make_fp8_kv_block(1, 8, 2, 128, device="cpu")
+    assert cache["k"].dtype == torch.float8_e4m3fn and cache["k_scale"].shape == (1, 8, 2, 1)
+    assert kvc.is_fp8_kv_cache(cache) and kvc.kv_storage_bytes(cache) == 2 * 8 * 2 * 128 + 2 * 8 * 2 * 4
+    good = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    bad = good.clone()
+    bad[0, 1, 1, 5] = float("nan")
+    before = cache["k"].view(torch.uint8).clone()
+    with pytest.raises(ValueError, match="non-finite"):
+        kvc.quantize_kv_pair_into(cache, good, bad, 0)
+    assert torch.equal(cache["k"].view(torch.uint8), before)   # K was not written either
+    with pytest.raises(ValueError, match="capacity"):
+        kvc.quantize_kv_pair_into(cache, good, good, 6)
+    with pytest.raises(ValueError, match="must match"):
+        kvc.quantize_kv_pair_into(cache, good, good[:, :3], 0)
+    with pytest.raises(TypeError):
+        kvc.quantize_kv_into(cache, "k", good.float(), 0)
+    with pytest.raises(ValueError, match="Invalid KV key"):
+        kvc.quantize_kv_into(cache, "q", good, 0)
+    with pytest.raises(ValueError, match="valid length"):
+        kvc.dequantize_kv(cache, "k", 9)
+    i8 = kvc.make_int8_kv_block(1, 8, 2, 128, device="cpu")
+    assert i8["k"].dtype == torch.int8 and kvc.is_quantized_kv_cache(i8)
+
+
+def test_storage_format_dispatch():
+    st = pkg_module("kv_cache_storage")
+    kvc = pkg_module("fp8_kv_cache")
+    assert st.cache_format(kvc.make_fp8_kv_block(1, 2, 1, 128, device="cpu")) == "fp8"
+    assert st.cache_format(kvc.make_int8_kv_block(1, 2, 1, 128, device="cpu")) == "int8"
+    assert st.cache_format({"k": torch.zeros(1, 2, 1, 128, dtype=torch.bfloat16)}) == "none"
+
+    class Inf:
+        kv_cache_quantization = "fp8"
+    assert st.quantization_mode(Inf) == "fp8"
+    Inf.kv_cache_quantization = "int4"
+    with pytest.raises(ValueError):
+        st.quantization_mode(Inf)
+    audit = st.cache_storage_audit(kvc.make_fp8_kv_block(1, 4, 2, 128, device="cpu"))
+    assert audit["gpu_storage_bytes"] == 2 * 4 * 2 * 128 + 2 * 4 * 2 * 4
+
+
+def test_serialized_fp8_validation_and_dtype_preserving_apply():
+    pf = pkg_module("pixelumm_fp8")
+    w = torch.zeros(256, 128, dtype=torch.float8_e4m3fn)
+    s = torch.ones(2, 1, dtype=torch.float32)
+    m = pf.FP8Linear.from_quantized(w, s, (256, 128))
+    m.to(dtype=torch.bfloat16)
+    assert m.fp8_weight.dtype == torch.float8_e4m3fn and m.fp8_scale.dtype == torch.float32
+    assert pf.CutlassFP8Linear is pf.FP8Linear
+    with pytest.raises(ValueError):
+        pf.FP8Linear.from_quantized(w, s, (256, 100))
+    with pytest.raises(ValueError, match="positive"):
+        pf.FP8Linear.from_quantized(w, torch.zeros(2, 1), (256, 128))
+    m.train()
+    with pytest.raises(RuntimeError, match="inference"):
+        m(torch.zeros(4, 128, dtype=torch.bfloat16))

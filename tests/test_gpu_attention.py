@@ -1,0 +1,173 @@
+"""GPU parity of the FP8-KV chunk attention against the oracle's float64
+softmax(Q K^T / sqrt(D)) V with K, V = code * scale read from the same cache.
+Bar: max-abs 2e-2 and rel-L2 1e-2."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_bf16, bf16_bits, pkg_module, u8
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache_from_chunks(dev, n_chunks, chunk, H, D, seed, fmt="fp8", capacity=None):
+    """Config-2 generator per chunk: N(0,1) x per-head gain U(0.5, 4), written
+    chunk by chunk with the KV write kernel."""
+    kvc = pkg_module("fp8_kv_cache")
+    make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
+    cap = capacity or n_chunks * chunk
+    cache = make(1, cap, H, D, device=dev)
+    for c in range(n_chunks):
+        g = torch.Generator(device=dev).manual_seed(seed + c)
+        gain = torch.empty(H, device=dev).uniform_(0.5, 4.0, generator=g)
+        k = (torch.randn(1, chunk, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        v = (torch.randn(1, chunk, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        kvc.quantize_kv_pair_into(cache, k, v, c * chunk)
+    return cache
+
+
+def _dequant(O, cache, n, fmt="fp8"):
+    dec = O.e4m3_decode if fmt == "fp8" else O.int8_decode
+    k = dec(u8(cache["k"][0, :n])) * cache["k_scale"][0, :n].cpu().numpy()
+    v = dec(u8(cache["v"][0, :n])) * cache["v_scale"][0, :n].cpu().numpy()
+    return k, v
+
+
+def _q(dev, Lq, H, D, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn(1, Lq, H, D, device=dev, generator=g).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("Lq,n_chunks,chunk,q_chunk0,fmt", [
+    (200, 3, 150, 1, "fp8"),       # Q spans chunks 1-2: partial tiles + the causal triangle
+    (128, 2, 128, 1, "fp8"),       # tile-aligned, Q is the last chunk: dense
+    (37, 4, 37, 3, "fp8"),         # tiny ragged chunk
+    (300, 3, 100, 0, "int8"),      # INT8-compat cache, Q over chunks 0-2
+])
+def test_chunk_attention_small(O, dev, Lq, n_chunks, chunk, q_chunk0, fmt):
+    print(f"case attn Lq={Lq} chunks={n_chunks}x{chunk} q0={q_chunk0} {fmt}", flush=True)
+    ca = pkg_module("cache_attention")
+    H, D = 3, 128
+    cache = _cache_from_chunks(dev, n_chunks, chunk, H, D, 100 + Lq, fmt)
+    kv_len = n_chunks * chunk
+    q = _q(dev, Lq, H, D, Lq)
+    q_pos0 = q_chunk0 * chunk
+    out = ca.chunk_attention(q, cache, kv_len, q_pos0=q_pos0, chunk_len=chunk)
+    kh, vh = _dequant(O, cache, kv_len, fmt)
+    vis = O.block_causal_visible(np.arange(q_pos0, q_pos0 + Lq), np.arange(kv_len), chunk)
+    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kh, vh, visible=vis)
+    assert_close_bf16(out[0].float().cpu().numpy(), ref, what="chunk attention")
+
+
+def test_chunk_attention_with_bf16_tail(O, dev):
+    """Denoising-pass form: FP8 history + the current chunk's bf16 K/V, full visibility."""
+    ca = pkg_module("cache_attention")
+    H, D, chunk = 2, 128, 160
+    cache = _cache_from_chunks(dev, 2, chunk, H, D, 7)
+    g = torch.Generator(device=dev).manual_seed(9)
+    kc = (torch.randn(1, chunk, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    vc = (torch.randn(1, chunk, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    q = _q(dev, chunk, H, D, 3)
+    out = ca.chunk_attention(q, cache, 2 * chunk, k_cur=kc, v_cur=vc)
+    kh, vh = _dequant(O, cache, 2 * chunk)
+    kall = np.concatenate([kh, O.bf16_bits_to_f32(bf16_bits(kc[0]))], 0)
+    vall = np.concatenate([vh, O.bf16_bits_to_f32(bf16_bits(vc[0]))], 0)
+    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kall, vall)
+    assert_close_bf16(out[0].float().cpu().numpy(), ref, what="attention + tail")
+    # tail only (empty cache prefix)
+    out2 = ca.chunk_attention(q, cache, 0, k_cur=kc, v_cur=vc)
+    ref2 = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kall[2 * chunk:], vall[2 * chunk:])
+    assert_close_bf16(out2[0].float().cpu().numpy(), ref2, what="tail only")
+
+
+def test_chunk_attention_config3_sampled_rows(O, dev):
+    """Q [1, 10800, 24, 128] of the last chunk over an 8-chunk
+    (86400-token) FP8 cache, scale 1/sqrt(128). 96 query rows checked, all heads."""
+    print("case attn config3", flush=True)
+    ca = pkg_module("cache_attention")
+    H, D, chunk, n = 24, 128, 10800, 8
+    cache = _cache_from_chunks(dev, n, chunk, H, D, 1000)
+    q = _q(dev, chunk, H, D, 77)
+    kv_len = n * chunk
+    out = ca.chunk_attention(q, cache, kv_len, q_pos0=(n - 1) * chunk, chunk_len=chunk)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    rows = np.concatenate([np.arange(0, 32), np.arange(5400, 5432), np.arange(10768, 10800)])
+    kh, vh = _dequant(O, cache, kv_len)
+    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh)
+    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="config 3")
+
+
+def test_chunk_attention_two_chunk_queries_triangle(O, dev):
+    """Multi-chunk Q at config-3 geometry (2 chunks of 10800 over 3 cached chunks):
+    rows on both sides of the chunk boundary."""
+    ca = pkg_module("cache_attention")
+    H, D, chunk = 2, 128, 10800
+    cache = _cache_from_chunks(dev, 3, chunk, H, D, 55)
+    q = _q(dev, 2 * chunk, H, D, 5)
+    out = ca.chunk_attention(q, cache, 3 * chunk, q_pos0=chunk, chunk_len=chunk)
+    rows = np.concatenate([np.arange(10780, 10820), np.arange(21560, 21600)])
+    kh, vh = _dequant(O, cache, 3 * chunk)
+    vis = O.block_causal_visible(chunk + rows, np.arange(3 * chunk), chunk)
+    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh, visible=vis)
+    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="triangle")
+
+
+def test_attention_invariants(dev):
+    """Constant V -> O = V; no visible key -> zeros."""
+    kvc = pkg_module("fp8_kv_cache")
+    ca = pkg_module("cache_attention")
+    H, D, L = 2, 128, 300
+    cache = kvc.make_fp8_kv_block(1, L, H, D, device=dev)
+    k = torch.randn(1, L, H, D, device=dev).to(torch.bfloat16)
+    vrow = torch.randn(1, 1, H, D, device=dev).to(torch.bfloat16)
+    kvc.quantize_kv_pair_into(cache, k, vrow.expand(1, L, H, D).contiguous(), 0)
+    q = torch.randn(1, 50, H, D, device=dev).to(torch.bfloat16)
+    out = ca.chunk_attention(q, cache, L)
+    vdq = kvc.dequantize_kv(cache, "v", 1)
+    assert torch.allclose(out.float(), vdq.float().expand(1, 50, H, D), atol=2e-2, rtol=0)
+    empty = ca.chunk_attention(q, cache, 0)
+    assert (empty == 0).all()
+
+
+def test_attention_is_deterministic(dev):
+    ca = pkg_module("cache_attention")
+    cache = _cache_from_chunks(dev, 2, 500, 4, 128, 3)
+    q = _q(dev, 500, 4, 128, 1)
+    a = ca.chunk_attention(q, cache, 1000, q_pos0=500, chunk_len=500)
+    b = ca.chunk_attention(q, cache, 1000, q_pos0=500, chunk_len=500)
+    assert torch.equal(a, b)
+
+
+def test_causal_attention_with_cache_mp_matches_reference_semantics(O, dev):
+    """The cached-attention entry point (update and denoise passes) against the
+    reference composition [decoded history | current img + txt] (nomas_cpt.py:614-625)."""
+    ca = pkg_module("cache_attention")
+    kvc = pkg_module("fp8_kv_cache")
+    H, D, Li, Lt = 2, 128, 96, 16
+    cache = kvc.make_fp8_kv_block(1, 400, H, D, device=dev)
+    mask = torch.zeros(1, 400, dtype=torch.bool, device=dev)
+    valid = 0
+    g = torch.Generator(device=dev).manual_seed(4)
+
+    def rnd(L):
+        return torch.randn(1, L, H, D, device=dev, generator=g).to(torch.bfloat16)
+
+    for step, update in enumerate([True, False, True]):
+        q, k, v = (rnd(Li), rnd(Lt)), (rnd(Li), rnd(Lt)), (rnd(Li), rnd(Lt))
+        hist_k, hist_v = _dequant(O, cache, valid)
+        with torch.no_grad():
+            img, txt = ca.causal_attention_with_cache_mp(q, k, v, cache, valid, "flash3", None,
+                                                         update, True, mask)
+        cur_k = np.concatenate([O.bf16_bits_to_f32(bf16_bits(t[0])) for t in k], 0)
+        cur_v = np.concatenate([O.bf16_bits_to_f32(bf16_bits(t[0])) for t in v], 0)
+        kall = np.concatenate([hist_k, cur_k], 0)
+        vall = np.concatenate([hist_v, cur_v], 0)
+        qall = np.concatenate([O.bf16_bits_to_f32(bf16_bits(t[0])) for t in q], 0)
+        ref = O.attention_reference(qall, kall, vall).reshape(Li + Lt, H * D)
+        got = torch.cat([img[0], txt[0]], 0).float().cpu().numpy()
+        assert img.shape == (1, Li, H * D) and txt.shape == (1, Lt, H * D)
+        assert_close_bf16(got, ref, what=f"cached attention step {step}")
+        if update:
+            assert mask[0, valid:valid + Li + Lt].all()
+            valid += Li + Lt

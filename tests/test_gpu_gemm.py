@@ -1,0 +1,157 @@
+"""GPU parity of the FP8 GEMMs against the oracle's dequantize-then-matmul
+(float64). Bars: max-abs 2e-2 and rel-L2 1e-2 (north star); the blockwise
+GEMM additionally meets the reference test's own bound, rel-L2 < 0.004
+(tests/inference/test_pixelumm_decoder_optimizations.py:201-221)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_close_bf16, bf16_bits, pkg_module, u8
+
+pytestmark = pytest.mark.gpu
+
+
+def _config1_inputs(M, K, N, seed=1234):
+    """BASELINE config 1 generators: X ~ N(0,1) with 0.1% outliers x20,
+    W ~ N(0, 0.02), bias ~ N(0, 0.01), one CPU generator per tensor. For
+    K > 3072 the weight std shrinks by sqrt(3072 / K) so that |Y| stays below
+    8, where bf16's half-ulp (<= 0.0156) fits the 2e-2 bar."""
+    w_std = 0.02 * min(1.0, (3072 / K) ** 0.5)
+    gx = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=gx)
+    x = torch.where(torch.rand(M, K, generator=gx) < 0.001, x * 20, x).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=torch.Generator().manual_seed(seed + 1)) * w_std).to(torch.bfloat16)
+    b = (torch.randn(N, generator=torch.Generator().manual_seed(seed + 2)) * 0.01).to(torch.bfloat16)
+    return x, w, b
+
+
+def _check_linear(O, dev, M, K, N, gelu, bias=True, rows=None):
+    ops = pkg_module("ops")
+    x, w, b = _config1_inputs(M, K, N, seed=M + 7 * K + N)
+    qw, sw = ops.quantize_rows_fp8(w.to(dev))
+    y = ops.linear_fp8(x.to(dev), qw, sw, b.to(dev) if bias else None, 1 if gelu else 0)
+    qx, sx = ops.quantize_rows_fp8(x.to(dev))
+    qxo, sxo = O.quantize_rows_fp8(bf16_bits(x))
+    qwo, swo = O.quantize_rows_fp8(bf16_bits(w))
+    assert np.array_equal(u8(qx), qxo) and np.array_equal(u8(qw), qwo)
+    assert np.array_equal(sx.cpu().numpy(), sxo) and np.array_equal(sw.cpu().numpy(), swo)
+    sel = np.arange(M) if rows is None else rows
+    ref = O.linear_reference(qxo[sel], sxo[sel], qwo, swo,
+                             O.bf16_bits_to_f32(bf16_bits(b)) if bias else None, gelu=gelu)
+    got = y.float().cpu().numpy()[sel]
+    return assert_close_bf16(got, ref, what=f"linear {M}x{K}x{N} gelu={gelu}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 128), (129, 256, 384), (300, 384, 256), (64, 12288, 3072)])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_linear_fp8_small_shapes(O, dev, M, K, N, gelu):
+    print(f"case linear {M}x{K}x{N} gelu={gelu}", flush=True)
+    _check_linear(O, dev, M, K, N, gelu)
+
+
+def test_linear_fp8_config1_full(O, dev):
+    """X [4096, 3072] x W [3072, 3072] + bias."""
+    print("case linear config1", flush=True)
+    _check_linear(O, dev, 4096, 3072, 3072, gelu=False)
+
+
+def test_linear_fp8_north_star_sampled_rows(O, dev):
+    """[10800 x 3072] x [3072 x 12288] with GELU; 600 rows checked (incl. the
+    ragged last M tile)."""
+    print("case linear north star", flush=True)
+    rows = np.concatenate([np.arange(0, 200), np.arange(5300, 5500), np.arange(10600, 10800)])
+    _check_linear(O, dev, 10800, 3072, 12288, gelu=True, rows=rows)
+
+
+def test_linear_fp8_no_bias_and_strided_out(O, dev):
+    ops = pkg_module("ops")
+    _check_linear(O, dev, 200, 256, 128, gelu=False, bias=False)
+    # row stride ldc > N through the C ABI
+    L = pkg_module("_lib")
+    a = torch.randint(0, 120, (70, 256), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (128, 256), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    sa = torch.rand(70, device=dev) + 0.5
+    sb = torch.rand(128, device=dev) + 0.5
+    out = torch.full((70, 136), 3.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.load().hn_gemm_fp8_rowcol(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+                                        None, out.data_ptr(), 70, 128, 256, 136, 0,
+                                        torch.cuda.current_stream().cuda_stream), "gemm")
+    ref = ops.gemm_fp8_rowcol(a, b, sa, sb)
+    assert torch.equal(out[:, :128], ref)
+    assert (out[:, 128:] == 3.0).all()
+
+
+def test_gemm_rowcol_is_deterministic(dev):
+    ops = pkg_module("ops")
+    a = torch.randint(0, 120, (1000, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (512, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    sa = torch.rand(1000, device=dev)
+    sb = torch.rand(512, device=dev)
+    assert torch.equal(ops.gemm_fp8_rowcol(a, b, sa, sb), ops.gemm_fp8_rowcol(a, b, sa, sb))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 128), (129, 256, 384), (2560, 4096, 4096), (4097, 128, 4096)])
+def test_blockwise_gemm_reference_harness(O, dev, m, n, k):
+    """The reference's own GEMM test (seed 44, a[:,128:256] *= 20, b[:128] *= 0.03)."""
+    print(f"case blockwise gemm {m}x{n}x{k}", flush=True)
+    pf = pkg_module("pixelumm_fp8")
+    torch.manual_seed(44)
+    a = torch.randn(m, k).to(torch.bfloat16)
+    b = torch.randn(n, k).to(torch.bfloat16)
+    a[:, 128:256] *= 20
+    b[:128] *= 0.03
+    qa, sa = pf._quantize_blockwise(a.to(dev))
+    qb, sb = pf._quantize_blockwise(b.to(dev))
+    actual = pf.load_extension().gemm(qa, qb, sa, sb)
+    expected = O.blockwise_gemm_reference(u8(qa), sa.cpu().numpy(), u8(qb), sb.cpu().numpy())
+    got = actual.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rel = np.linalg.norm(got - expected) / np.linalg.norm(expected)
+    assert rel < 0.004, rel
+    # and the bf16 rounding bound of the output itself
+    assert np.all(np.abs(got - expected) <= np.abs(expected) * 2 ** -8 + 1e-3 * np.abs(expected).max())
+
+
+def test_blockwise_gemm_contract_errors(dev):
+    pf = pkg_module("pixelumm_fp8")
+    ext = pf.load_extension()
+    a = torch.zeros(64, 256, dtype=torch.float8_e4m3fn, device=dev)
+    b = torch.zeros(128, 256, dtype=torch.float8_e4m3fn, device=dev)
+    sa = torch.ones(1, 2, device=dev)
+    sb = torch.ones(1, 2, device=dev)
+    assert ext.gemm(a, b, sa, sb).shape == (64, 128)
+    with pytest.raises(RuntimeError, match="Invalid activation scales"):
+        ext.gemm(a, b, torch.ones(2, 2, device=dev), sb)
+    with pytest.raises(RuntimeError, match="Invalid GEMM shape"):
+        ext.gemm(a, torch.zeros(96, 256, dtype=torch.float8_e4m3fn, device=dev), sa, sb)
+    with pytest.raises(RuntimeError, match="E4M3"):
+        ext.gemm(a.view(torch.uint8), b, sa, sb)
+
+
+def test_fp8_linear_modules(O, dev):
+    """FP8Linear (decoder, blockwise) and FP8StoredLinear (DiT, per-channel)
+    forwards against the oracle."""
+    pf = pkg_module("pixelumm_fp8")
+    dl = pkg_module("dit_fp8_linear")
+    torch.manual_seed(3)
+    lin = torch.nn.Linear(256, 384, bias=False).to(dev, torch.bfloat16).eval()
+    m = pf.FP8Linear(lin)
+    x = torch.randn(2, 65, 256, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y = m(x)
+    assert y.shape == (2, 65, 384)
+    qa, sa = O.quantize_blockwise_fp8(bf16_bits(x.reshape(-1, 256)))
+    ref = O.blockwise_gemm_reference(qa, sa, u8(m.fp8_weight), m.fp8_scale.cpu().numpy())
+    assert_close_bf16(y.reshape(-1, 384).float().cpu().numpy(), ref, what="FP8Linear")
+    assert pf.execution_stats()[-1]["calls"] >= 1
+
+    lin2 = torch.nn.Linear(256, 128).to(dev, torch.bfloat16)
+    d = dl.FP8StoredLinear(lin2)
+    with torch.no_grad():
+        y2 = d(x)
+    qx, sx = O.quantize_rows_fp8(bf16_bits(x.reshape(-1, 256)))
+    ref2 = O.linear_reference(qx, sx, u8(d.weight_q), d.weight_scale.cpu().numpy(),
+                              O.bf16_bits_to_f32(bf16_bits(lin2.bias)))
+    assert_close_bf16(y2.reshape(-1, 128).float().cpu().numpy(), ref2, what="FP8StoredLinear")
+    with pytest.raises(TypeError):
+        d(x.float())

@@ -1,0 +1,140 @@
+"""GPU parity of the quantizers: codes and scales bit-exact against the C oracle."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits, pkg_module, u8
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 8), (7, 3072), (300, 2048), (64, 12288), (5, 16384), (33, 136)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_rows_fp8_bit_exact(O, dev, rows, cols, mode):
+    print(f"case rows_fp8 {rows}x{cols} mode={mode}", flush=True)
+    ops = pkg_module("ops")
+    x = _gen((rows, cols), rows * 31 + cols, 3.0)
+    x[::3, : cols // 2] *= 1e-3
+    if rows > 2:
+        x[1] = 0
+    q, s = ops.quantize_rows_fp8(x.to(dev), mode, 1e-4)
+    qo, so = O.quantize_rows_fp8(bf16_bits(x), mode)
+    assert np.array_equal(u8(q), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_rows_fp8_special_values(O, dev):
+    print("case rows_fp8 special values", flush=True)
+    ops = pkg_module("ops")
+    bits = np.zeros((6, 64), np.uint16)
+    bits[0, :] = 0x0001                      # bf16 subnormals
+    bits[1, ::2] = 0x8003
+    bits[2, 5] = 0x3F80                      # single non-zero (1.0)
+    bits[3, :] = np.arange(64, dtype=np.uint16) * 0x0101   # mixed patterns, finite
+    bits[3] &= 0x7F7F
+    bits[4, :] = 0x43E0                      # 448 everywhere
+    bits[5, :] = 0x0000                      # zero row
+    x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    for mode in (0, 1):
+        q, s = ops.quantize_rows_fp8(x.to(dev), mode, 1e-4)
+        qo, so = O.quantize_rows_fp8(bits, mode)
+        assert np.array_equal(u8(q), qo)
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_rows_fp8_strided_input(O, dev):
+    ops = pkg_module("ops")
+    x = _gen((64, 512), 11)
+    view = x.to(dev)[:, 128:384]            # row stride 512, 16-byte aligned start
+    q, s = ops.quantize_rows_fp8(view, 0, 1e-4)
+    qo, so = O.quantize_rows_fp8(bf16_bits(x[:, 128:384]))
+    assert np.array_equal(u8(q), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("m,k", [(1, 128), (129, 256), (300, 384), (4096, 3072), (4097, 128)])
+def test_blockwise_fp8_bit_exact(O, dev, m, k):
+    print(f"case blockwise {m}x{k}", flush=True)
+    ops = pkg_module("ops")
+    x = _gen((m, k), m + k)
+    if k > 128:
+        x[:, 128:256] *= 20
+    q, s = ops.quantize_blockwise_fp8(x.to(dev))
+    qo, so = O.quantize_blockwise_fp8(bf16_bits(x))
+    assert np.array_equal(u8(q), qo)
+    assert np.array_equal(s.cpu().numpy(), so)
+
+
+def _kv_inputs(B, H, L, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    gain = torch.empty(H).uniform_(0.5, 4.0, generator=g)
+    x = torch.randn(B, H, L, D, generator=g) * gain[None, :, None, None]
+    return x.to(torch.bfloat16)                 # [B, H, L, D] memory (config-2 layout)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_kv_quantize_config2_full_size_bit_exact(O, dev, fmt):
+    """K, V [1, 24, 10800, 128] written at chunk slot 2 of a
+    3-chunk cache; every code and scale compared."""
+    print(f"case kv config2 {fmt}", flush=True)
+    kvc = pkg_module("fp8_kv_cache")
+    B, H, L, D = 1, 24, 10800, 128
+    k = _kv_inputs(B, H, L, D, 1)
+    v = _kv_inputs(B, H, L, D, 2)
+    make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
+    cache = make(B, 3 * L, H, D, device=dev)
+    for t in cache.values():
+        t.view(torch.uint8).fill_(0xAB)
+    kd, vd = k.to(dev).transpose(1, 2), v.to(dev).transpose(1, 2)   # [B, L, H, D] views
+    kvc.quantize_kv_pair_into(cache, kd, vd, 2 * L)
+    torch.cuda.synchronize()
+    f = O.KV_FP8 if fmt == "fp8" else O.KV_INT8
+    for name, x in (("k", k), ("v", v)):
+        qo, so = O.kv_quantize(np.transpose(bf16_bits(x), (0, 2, 1, 3)), f)
+        got = u8(cache[name])
+        assert np.array_equal(got[:, 2 * L:], qo), f"{name} codes"
+        assert (got[:, :2 * L] == 0xAB).all(), f"{name}: bytes before `start` were touched"
+        gs = cache[name + "_scale"].cpu().numpy()
+        assert np.array_equal(gs[:, 2 * L:].view(np.uint32), so.view(np.uint32)), f"{name} scales"
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_kv_dequantize_matches_oracle(O, dev, fmt):
+    kvc = pkg_module("fp8_kv_cache")
+    B, H, L, D = 2, 3, 70, 128
+    make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
+    cache = make(B, 100, H, D, device=dev)
+    k = _kv_inputs(B, H, L, D, 5).transpose(1, 2).contiguous()
+    kvc.quantize_kv_pair_into(cache, k.to(dev), k.to(dev), 0)
+    y = kvc.dequantize_kv(cache, "k", 65)
+    f = O.KV_FP8 if fmt == "fp8" else O.KV_INT8
+    ref = O.kv_dequantize(u8(cache["k"])[:, :65], cache["k_scale"].cpu().numpy()[:, :65], f)
+    assert np.array_equal(bf16_bits(y), ref)
+    assert kvc.dequantize_kv(cache, "v", 0).shape == (B, 0, H, D)
+
+
+def test_kv_write_rejects_non_finite_before_writing(dev):
+    kvc = pkg_module("fp8_kv_cache")
+    cache = kvc.make_fp8_kv_block(1, 16, 2, 128, device=dev)
+    cache["k"].view(torch.uint8).fill_(7)
+    k = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16, device=dev)
+    v = k.clone()
+    v[0, 2, 1, 9] = float("inf")
+    with pytest.raises(ValueError, match="non-finite"):
+        kvc.quantize_kv_pair_into(cache, k, v, 0)
+    assert (u8(cache["k"]) == 7).all()
+
+
+def test_kv_write_twice_is_deterministic(dev):
+    kvc = pkg_module("fp8_kv_cache")
+    x = _kv_inputs(1, 4, 500, 128, 9).transpose(1, 2).contiguous().to(dev)
+    a = kvc.make_fp8_kv_block(1, 500, 4, 128, device=dev)
+    b = kvc.make_fp8_kv_block(1, 500, 4, 128, device=dev)
+    kvc.quantize_kv_pair_into(a, x, x, 0)
+    kvc.quantize_kv_pair_into(b, x, x, 0)
+    assert torch.equal(a["k"].view(torch.uint8), b["k"].view(torch.uint8))
+    assert torch.equal(a["v_scale"], b["v_scale"])

@@ -1,0 +1,310 @@
+"""Pins for the CPU oracle (no GPU). Each check is independent of the oracle's
+own formulas: torch's float8_e4m3fn cast (a library routine), hand-derived
+known answers, invariants, and brute force on tiny inputs."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_bits
+
+
+def _torch_e4m3(f32: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(f32, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+# ---------------------------------------------------------------- e4m3 codec
+
+def test_e4m3_encode_all_bf16_patterns_match_torch(O):
+    f = O.bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    assert np.array_equal(O.e4m3_encode(f), _torch_e4m3(f))
+
+
+def test_e4m3_encode_random_fp32_patterns_match_torch(O):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2 ** 32, size=1 << 22, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    assert np.array_equal(O.e4m3_encode(f), _torch_e4m3(f))
+    # dense sweep of the finite range the quantizers produce (|x/s| <= 448)
+    g = rng.uniform(-449, 449, size=1 << 22).astype(np.float32)
+    assert np.array_equal(O.e4m3_encode(g), _torch_e4m3(g))
+
+
+def test_e4m3_decode_matches_torch(O):
+    c = np.arange(256, dtype=np.uint8)
+    d = O.e4m3_decode(c)
+    t = torch.from_numpy(c.copy()).view(torch.float8_e4m3fn).float().numpy()
+    same = (d == t) | (np.isnan(d) & np.isnan(t))
+    assert same.all()
+
+
+@pytest.mark.parametrize("x,code", [
+    (0.0, 0x00), (-0.0, 0x80), (448.0, 0x7E), (-448.0, 0xFE),
+    (464.0, 0x7E),            # tie between 448 and the NaN step -> even (448)
+    (465.0, 0x7F), (480.0, 0x7F), (1e9, 0x7F), (float("inf"), 0x7F), (float("-inf"), 0xFF),
+    (2.0 ** -9, 0x01),        # smallest subnormal
+    (2.0 ** -10, 0x00),       # half of it: tie -> even (0)
+    (1.5 * 2.0 ** -10, 0x01),
+    (3 * 2.0 ** -10, 0x02),   # tie between 1 and 2 subnormal steps -> even
+    (2.0 ** -6, 0x08),        # smallest normal
+    (1.0, 0x38), (1.0625, 0x38), (1.1875, 0x3A), (1.125, 0x39), (-2.5, 0xC2),
+    (240.0, 0x77), (256.0, 0x78),
+])
+def test_e4m3_known_answers(O, x, code):
+    assert int(O.lib().hn_oracle_e4m3_encode(x)) == code
+
+
+# ---------------------------------------------------------------- scale rules
+
+def _row_bits(vals):
+    return bf16_bits(torch.tensor(vals, dtype=torch.float32).to(torch.bfloat16)).reshape(1, -1)
+
+
+def test_row_quant_power_of_two_scale_known_answer(O):
+    # amax = 7 -> s = 7/448 = 2^-6 exactly, so x/s = 64 x exactly.
+    vals = [7.0, -3.5, 0.25, 0.0, 1.0 / 64, 3.0 / 128, -7.0, 0.1875]
+    q, s = O.quantize_rows_fp8(_row_bits(vals), O.SCALE_ZERO_ONE)
+    assert s[0] == np.float32(2.0 ** -6)
+    expect = [O.lib().hn_oracle_e4m3_encode(64.0 * v) for v in vals]
+    assert list(q[0]) == expect
+    assert q[0][0] == 0x7E and q[0][6] == 0xFE
+
+
+def test_row_quant_amax_448_is_identity(O):
+    vals = [448.0, 1.0, -2.0, 0.5, 3.0, 5.0, 6.0, 7.0]
+    q, s = O.quantize_rows_fp8(_row_bits(vals), O.SCALE_CLAMP)
+    assert s[0] == 1.0
+    assert list(q[0]) == [O.lib().hn_oracle_e4m3_encode(v) for v in vals]
+
+
+def test_row_quant_zero_and_tiny_rows(O):
+    zeros = np.zeros((1, 16), np.uint16)
+    q, s = O.quantize_rows_fp8(zeros, O.SCALE_ZERO_ONE)
+    assert s[0] == 1.0 and not q.any()
+    q, s = O.quantize_rows_fp8(zeros, O.SCALE_CLAMP)       # clamp_min(1e-4) / 448
+    assert s[0] == np.float32(np.float32(1e-4) / np.float32(448.0)) and not q.any()
+    tiny = _row_bits([1e-6] * 8)
+    q, s = O.quantize_rows_fp8(tiny, O.SCALE_CLAMP)        # amax < floor: x/s < 448
+    assert s[0] == np.float32(np.float32(1e-4) / np.float32(448.0))
+    assert (q[0] < 0x7E).all()
+    sub = np.array([[0x0001, 0x8003, 0x0000, 0x0002] * 2], np.uint16)  # bf16 subnormals
+    q, s = O.quantize_rows_fp8(sub, O.SCALE_ZERO_ONE)
+    assert s[0] > 0 and q[0][1] == 0xFE                   # amax element -> -448
+
+
+def test_row_quant_invariants_random(O):
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal((256, 384)).astype(np.float32) * rng.uniform(1e-3, 1e3, (256, 1)).astype(np.float32))
+    xb = bf16_bits(x.to(torch.bfloat16))
+    xf = O.bf16_bits_to_f32(xb)
+    for mode in (O.SCALE_CLAMP, O.SCALE_ZERO_ONE):
+        q, s = O.quantize_rows_fp8(xb, mode)
+        mag = q & 0x7F
+        assert (mag <= 0x7E).all()
+        amax_idx = np.argmax(np.abs(xf), axis=1)
+        assert (mag[np.arange(256), amax_idx] == 0x7E).all()
+        # reconstruction error within half an e4m3 step of x/s
+        t = xf / s[:, None]
+        d = O.e4m3_decode(q)
+        step = np.where(np.abs(t) < 2.0 ** -6, 2.0 ** -9, 2.0 ** (np.floor(np.log2(np.maximum(np.abs(t), 1e-30))) - 3))
+        assert (np.abs(t - d) <= step / 2 + 1e-7 * np.abs(t)).all()
+
+
+def test_row_quant_matches_torch_reference_recipe(O):
+    """The reference's CPU recipe run on torch ops (cutlass_fp8.py:35-41 with 1 x K
+    blocks; int8_kv_cache.py:150-152 rule with 448): independent division and cast."""
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((64, 3072)).astype(np.float32)).to(torch.bfloat16)
+    x[rng.random((64, 3072)) < 0.001] *= 20
+    xf = x.float()
+    s_lin = xf.abs().amax(dim=1, keepdim=True).clamp_min(1e-4) / 448.0
+    q_lin = (xf / s_lin).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    q, s = O.quantize_rows_fp8(bf16_bits(x), O.SCALE_CLAMP)
+    assert np.array_equal(q, q_lin) and np.array_equal(s, s_lin.numpy()[:, 0])
+    peak = xf.abs().amax(dim=1, keepdim=True)
+    s_kv = torch.where(peak > 0, peak / 448.0, torch.ones_like(peak))
+    q_kv = (xf / s_kv).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    q, s = O.quantize_rows_fp8(bf16_bits(x), O.SCALE_ZERO_ONE)
+    assert np.array_equal(q, q_kv) and np.array_equal(s, s_kv.numpy()[:, 0])
+
+
+def test_blockwise_quant_known_answers_and_padding(O):
+    m, k = 130, 256
+    x = np.zeros((m, k), np.float32)
+    x[0, 0] = 448.0          # block (0,0): s = 1
+    x[5, 130] = -7.0         # block (0,1): s = 2^-6
+    x[129, 3] = 0.5          # block (1,0): only row 129 is real, padding adds nothing
+    xb = bf16_bits(torch.from_numpy(x).to(torch.bfloat16))
+    q, s = O.quantize_blockwise_fp8(xb)
+    assert s.shape == (2, 2)
+    assert s[0, 0] == 1.0 and s[0, 1] == np.float32(2.0 ** -6)
+    assert s[1, 0] == np.float32(np.float32(0.5) / np.float32(448.0))
+    assert s[1, 1] == np.float32(np.float32(1e-4) / np.float32(448.0))
+    assert q[0, 0] == 0x7E and q[5, 130] == 0xFE and q[129, 3] == 0x7E
+    assert np.count_nonzero(q) == 3
+
+
+def test_blockwise_quant_matches_torch_reference_recipe(O):
+    rng = np.random.default_rng(4)
+    x = torch.from_numpy(rng.standard_normal((300, 384)).astype(np.float32)).to(torch.bfloat16)
+    m, k = x.shape
+    padded = torch.nn.functional.pad(x, (0, 0, 0, (-m) % 128))
+    blocks = padded.float().reshape(-1, 128, k // 128, 128)
+    scale = blocks.abs().amax(dim=(1, 3)).clamp_min(1e-4) / 448.0
+    qt = (blocks / scale[:, None, :, None]).to(torch.float8_e4m3fn).reshape(-1, k)[:m]
+    q, s = O.quantize_blockwise_fp8(bf16_bits(x))
+    assert np.array_equal(q, qt.view(torch.uint8).numpy())
+    assert np.array_equal(s, scale.numpy())
+
+
+# ---------------------------------------------------------------- KV cache
+
+def test_kv_quant_writes_at_offset_with_strides(O):
+    rng = np.random.default_rng(5)
+    B, L, H, D = 2, 5, 3, 128
+    vals = torch.from_numpy(rng.standard_normal((B, H, L, D)).astype(np.float32)).to(torch.bfloat16)
+    x_bhsd = bf16_bits(vals)                      # [B,H,L,D] memory
+    x_view = np.transpose(x_bhsd, (0, 2, 1, 3))  # logical [B,L,H,D], strided
+    cq = np.zeros((B, 12, H, D), np.uint8)
+    cs = np.zeros((B, 12, H, 1), np.float32)
+    O.kv_quantize_into(x_view, cq, cs, 4)
+    assert not cq[:, :4].any() and not cq[:, 9:].any()
+    q2, s2 = O.quantize_rows_fp8(np.ascontiguousarray(x_view).reshape(-1, D), O.SCALE_ZERO_ONE)
+    assert np.array_equal(cq[:, 4:9].reshape(-1, D), q2)
+    assert np.array_equal(cs[:, 4:9].reshape(-1), s2)
+
+
+def test_int8_compat_known_answers(O):
+    # amax 127 -> s = 1: round half away from zero, clamp +-127
+    vals = [127.0, 0.5, -0.5, 1.5, 2.5, -2.5, 0.0, -127.0] + [0.0] * 120
+    x = _row_bits(vals).reshape(1, 1, 1, 128)
+    q, s = O.kv_quantize(x, O.KV_INT8)
+    assert s.reshape(-1)[0] == 1.0
+    got = q.reshape(-1)[:8].view(np.int8).tolist()
+    assert got == [127, 1, -1, 2, 3, -3, 0, -127]
+
+
+def test_int8_compat_matches_torch_reference_recipe(O):
+    """int8_kv_cache.py:150-157 on torch ops."""
+    rng = np.random.default_rng(6)
+    x = torch.from_numpy(rng.standard_normal((4, 7, 3, 128)).astype(np.float32) * 3).to(torch.bfloat16)
+    src = x.float()
+    peak = src.abs().amax(dim=-1, keepdim=True)
+    s = torch.where(peak > 0, peak / 127.0, torch.ones_like(peak))
+    scaled = src / s
+    rounded = torch.where(scaled >= 0, torch.floor(scaled + 0.5), torch.ceil(scaled - 0.5))
+    qt = rounded.clamp(-127, 127).to(torch.int8)
+    q, so = O.kv_quantize(bf16_bits(x), O.KV_INT8)
+    assert np.array_equal(q.view(np.int8), qt.numpy())
+    assert np.array_equal(so, s.numpy())
+
+
+def test_int8_weight_quant_matches_torch_reference_recipe(O):
+    """int8_stored_bf16_linear.py:46-61 on torch ops (K not a multiple of 128)."""
+    rng = np.random.default_rng(7)
+    w = torch.from_numpy(rng.standard_normal((16, 200)).astype(np.float32) * 0.02)
+    n, k = w.shape
+    groups = (k + 127) // 128
+    padded = torch.nn.functional.pad(w, (0, groups * 128 - k))
+    rows = padded.reshape(n, groups, 128)
+    mx = rows.abs().amax(dim=-1)
+    scale = torch.where(mx > 0, mx / 127.0, 1.0)
+    norm = rows / scale.unsqueeze(-1)
+    qt = ((norm.abs() + 0.5).floor() * norm.sign()).clamp_(-127, 127).to(torch.int8).reshape(n, -1)[:, :k]
+    q, s = O.quantize_weight_int8(w.numpy())
+    assert np.array_equal(q, qt.numpy()) and np.array_equal(s, scale.numpy())
+
+
+def test_kv_dequant_is_bf16_of_product(O):
+    q = np.array([[0x38, 0x7E, 0x01, 0xB8]], np.uint8)     # 1, 448, 2^-9, -1
+    s = np.array([[3.0]], np.float32)
+    y = O.bf16_bits_to_f32(O.kv_dequantize(q, s))
+    assert y.tolist() == [[3.0, 1344.0, 3.0 * 2 ** -9, -3.0]]
+
+
+# ---------------------------------------------------------------- float references
+
+def test_linear_reference_brute_force(O):
+    rng = np.random.default_rng(8)
+    M, N, K = 3, 4, 128
+    qx = rng.integers(0, 256, (M, K), dtype=np.uint8) & 0xF7   # avoid NaN codes
+    qw = rng.integers(0, 256, (N, K), dtype=np.uint8) & 0xF7
+    sx = rng.uniform(0.1, 2, M).astype(np.float32)
+    sw = rng.uniform(0.1, 2, N).astype(np.float32)
+    b = rng.standard_normal(N)
+    y = O.linear_reference(qx, sx, qw, sw, b)
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                acc += float(O.lib().hn_oracle_e4m3_decode(int(qx[m, k]))) * float(O.lib().hn_oracle_e4m3_decode(int(qw[n, k])))
+            assert math.isclose(y[m, n], acc * float(sx[m]) * float(sw[n]) + b[n], rel_tol=1e-12, abs_tol=1e-12)
+    g = O.linear_reference(qx, sx, qw, sw, b, gelu=True)
+    t = torch.nn.functional.gelu(torch.from_numpy(y), approximate="tanh").numpy()
+    assert np.allclose(g, t, rtol=1e-12, atol=1e-12)
+
+
+def test_blockwise_gemm_reference_brute_force(O):
+    rng = np.random.default_rng(9)
+    M, N, K = 130, 128, 256
+    qa = rng.integers(0, 256, (M, K), dtype=np.uint8) & 0xF7
+    qb = rng.integers(0, 256, (N, K), dtype=np.uint8) & 0xF7
+    sa = rng.uniform(0.5, 2, (2, 2)).astype(np.float32)
+    sb = rng.uniform(0.5, 2, (1, 2)).astype(np.float32)
+    y = O.blockwise_gemm_reference(qa, sa, qb, sb)
+    da, db = O.e4m3_decode(qa).astype(np.float64), O.e4m3_decode(qb).astype(np.float64)
+    for (m, n) in [(0, 0), (129, 127), (64, 5), (128, 77)]:
+        acc = sum(float(sa[m // 128, kb]) * float(sb[n // 128, kb]) *
+                  float(np.dot(da[m, kb * 128:(kb + 1) * 128], db[n, kb * 128:(kb + 1) * 128]))
+                  for kb in range(2))
+        assert math.isclose(y[m, n], acc, rel_tol=1e-12, abs_tol=1e-9)
+
+
+def _attn_loops(q, k, v, vis, scale):
+    Lq, H, D = q.shape
+    out = np.zeros_like(q, dtype=np.float64)
+    for h in range(H):
+        for i in range(Lq):
+            js = [j for j in range(k.shape[0]) if vis[i][j]]
+            if not js:
+                continue
+            logits = [scale * sum(q[i, h, d] * k[j, h, d] for d in range(D)) for j in js]
+            mx = max(logits)
+            w = [math.exp(x - mx) for x in logits]
+            z = sum(w)
+            for d in range(D):
+                out[i, h, d] = sum(w[t] * v[js[t], h, d] for t in range(len(js))) / z
+    return out
+
+
+def test_attention_reference_brute_force_block_causal(O):
+    rng = np.random.default_rng(10)
+    Lq, Lk, H, D, chunk = 5, 9, 2, 4, 3
+    q = rng.standard_normal((Lq, H, D))
+    k = rng.standard_normal((Lk, H, D))
+    v = rng.standard_normal((Lk, H, D))
+    qpos = np.arange(4, 4 + Lq)                 # queries in chunks 1..2
+    vis = O.block_causal_visible(qpos, np.arange(Lk), chunk)
+    # independent enumeration of the chunk rule
+    for i, r in enumerate(qpos):
+        for p in range(Lk):
+            assert vis[i, p] == (p // chunk <= r // chunk)
+    got = O.attention_reference(q, k, v, visible=vis, scale=0.7)
+    assert np.allclose(got, _attn_loops(q, k, v, vis, 0.7), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_reference_invariants(O):
+    rng = np.random.default_rng(11)
+    Lq, Lk, H, D = 6, 20, 2, 8
+    q = rng.standard_normal((Lq, H, D))
+    k = rng.standard_normal((Lk, H, D))
+    v = np.broadcast_to(rng.standard_normal((1, H, D)), (Lk, H, D)).copy()
+    assert np.allclose(O.attention_reference(q, k, v), v[:Lq], atol=1e-12)   # constant V
+    k2 = k.copy()
+    k2[7] = 1e3 * q[0]                                                      # one dominant logit
+    v2 = rng.standard_normal((Lk, H, D))
+    o = O.attention_reference(q[:1], k2, v2)
+    assert np.allclose(o[0], v2[7], atol=1e-9)
+    none = O.attention_reference(q, k, v2, key_valid=np.zeros(Lk, bool))
+    assert not none.any()                                                   # no visible key -> zeros
