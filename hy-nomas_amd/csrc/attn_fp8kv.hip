@@ -6,21 +6,23 @@
 // head); each wave owns 32 queries (one 32-column MFMA block), and two
 // workgroups share a CU (2 waves per SIMD), so one wave's softmax VALU work
 // overlaps the other's MFMAs. Keys stream
-// through LDS in tiles of 64: the cache segment's 1-byte codes are widened to
-// bf16 once per workgroup while they are written to LDS (exact: every e4m3
-// and int8 code is a bf16 value), and the per-token fp32 scales are staged
-// beside them. The scales never touch the bf16 operands: the K scale (times
-// softmax_scale * log2 e) multiplies the fp32 logits and the V scale
-// multiplies the fp32 probabilities before they are packed for the PV MFMA,
-// so K and V enter as code * scale in fp32 -- not rounded to bf16 first. The
-// optional unquantized tail (the current chunk's bf16 K/V) is copied into the
-// same LDS format with unit scales, so one compute path serves both segments.
+// through LDS in tiles of 64. K codes are widened to bf16 once per workgroup
+// as they are written to LDS (exact: every e4m3 and int8 code is a bf16
+// value) and the per-token K scale (times softmax_scale * log2 e) multiplies
+// the fp32 logits, so K enters as code * scale in fp32. V is dequantized once
+// per workgroup into fp16, fp16(code * scale) -- the value range of the
+// original activations, where fp16 keeps 11 significant bits -- and P stays in
+// [0, 1] as fp16, so the PV product carries 2^-11 relative rounding instead of
+// bf16's 2^-8. The optional unquantized tail (the current chunk's bf16 K/V) is
+// copied into the same LDS formats with unit K scales, so one compute path
+// serves both segments.
 //
 // Per tile the wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: the
 // MFMA output puts one query per lane column, so the online-softmax max/sum
-// are lane-local plus one exchange with lane ^ 32. P^T is packed to bf16 in
-// registers and reused as the B operand of O^T += V^T P^T (V^T is transposed
-// into LDS with a key order that matches the S^T register layout). Two LDS
+// are lane-local plus one exchange with lane ^ 32. P^T is packed to fp16 in
+// registers and reused as the B operand of O^T += V^T P^T on
+// v_mfma_f32_32x32x16_f16 (V^T is transposed into LDS with a key order that
+// matches the S^T register layout). Two LDS
 // stages: the next tile's global loads are in flight in registers while the
 // MFMAs consume the current one.
 //
@@ -41,10 +43,10 @@ constexpr int NT = 64 * NW;
 constexpr int QW = 32;             // queries per wave
 constexpr int BQ = QW * NW;        // queries per workgroup
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
-constexpr int VROW = BKV * 2 + 16; // V^T tile row: 64 bf16 + 16 B pad
+constexpr int VROW = BKV * 2 + 16; // V^T tile row: 64 fp16 + 16 B pad
 constexpr int K_BYTES = BKV * KROW;
 constexpr int V_BYTES = D * VROW;
-constexpr int S_BYTES = 2 * BKV * 4;  // per-key K and V scales (fp32)
+constexpr int S_BYTES = BKV * 4;  // per-key K scales (fp32)
 constexpr int STAGE = K_BYTES + V_BYTES + S_BYTES;
 
 struct Params {
@@ -102,6 +104,37 @@ HN_DEVICE void cvt16(const uint4& c, int fmt, uint32_t (&o)[8]) {
     }
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+HN_DEVICE uint32_t pack_f16(float a, float b) {
+    const f32x2 f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+}
+
+// 16 codes (one uint4) -> 16 fp16 of code * s (fp32 product, one RNE), 8 dwords.
+HN_DEVICE void dequant16_f16(const uint4& c, float s, int fmt, uint32_t (&o)[8]) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (fmt == HN_KV_FP8) {
+            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], false);
+            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], true);
+            o[2 * i] = pack_f16(lo.x * s, lo.y * s);
+            o[2 * i + 1] = pack_f16(hi.x * s, hi.y * s);
+        } else {
+            o[2 * i] = pack_f16((float)(int8_t)(w[i] & 0xffu) * s, (float)(int8_t)((w[i] >> 8) & 0xffu) * s);
+            o[2 * i + 1] = pack_f16((float)(int8_t)((w[i] >> 16) & 0xffu) * s, (float)(int8_t)(w[i] >> 24) * s);
+        }
+    }
+}
+
+// Two bf16 (one dword) -> two fp16.
+HN_DEVICE uint32_t bf16x2_to_f16x2(uint32_t w) {
+    return pack_f16(bf16_bits_to_f32(w & 0xffffu), bf16_bits_to_f32(w >> 16));
+}
+
 // Registers holding one cache tile between its global load and its LDS
 // write (the load is issued before the tile in LDS is consumed).
 // K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
@@ -150,7 +183,7 @@ HN_DEVICE void store_vt(uint8_t* vl, const uint32_t (&cv)[2][8]) {
     }
 }
 
-// Per-key scales in LDS: [0, 64) K scale * softmax_scale * log2 e, [64, 128) V scale.
+// Per-key scales in LDS: K scale * softmax_scale * log2 e.
 HN_DEVICE float* stage_scales(uint8_t* st) { return reinterpret_cast<float*>(st + K_BYTES + V_BYTES); }
 
 HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st) {
@@ -168,12 +201,8 @@ HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st
     }
     uint32_t cv[2][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) cvt16(r.v[i], p.fmt, cv[i]);
+    for (int i = 0; i < 2; ++i) dequant16_f16(r.v[i], r.sv[i], p.fmt, cv[i]);
     store_vt(st + K_BYTES, cv);
-    if ((t & 7) == 0) {
-        sc[BKV + (t >> 3) * 2] = r.sv[0];
-        sc[BKV + (t >> 3) * 2 + 1] = r.sv[1];
-    }
 }
 
 // Unquantized tail tile (bf16 K/V of the current chunk): load and write to LDS
@@ -202,13 +231,13 @@ HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t fir
         const uint16_t* src = p.vcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + dg * 16;
         const uint4 lo = *reinterpret_cast<const uint4*>(src);
         const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
-        cv[i][0] = lo.x; cv[i][1] = lo.y; cv[i][2] = lo.z; cv[i][3] = lo.w;
-        cv[i][4] = hi.x; cv[i][5] = hi.y; cv[i][6] = hi.z; cv[i][7] = hi.w;
+        const uint32_t b[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[i][e] = bf16x2_to_f16x2(b[e]);
     }
     store_vt(st + K_BYTES, cv);
     float* sc = stage_scales(st);
     if (t < BKV) sc[t] = p.scale_log2;
-    else if (t < 2 * BKV) sc[t] = 1.0f;
 }
 
 HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -266,7 +295,11 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     const int n_cache = (int)((cache_end + BKV - 1) / BKV);
     const int n_tail = tail_end > 0 ? (int)((tail_end + BKV - 1) / BKV) : 0;
     const int n_tiles = n_cache + n_tail;
-    const int64_t qchunk = p.chunk > 0 ? qpos / p.chunk : 0;
+    // Visibility limits (exclusive key positions): this lane's query, and the
+    // workgroup's first query (every key below it is visible to all lanes).
+    const int64_t no_limit = p.kv_len + p.cur_len;
+    const int64_t key_limit = p.chunk > 0 ? (qpos / p.chunk + 1) * p.chunk : no_limit;
+    const int64_t wg_key_limit = p.chunk > 0 ? (r_first / p.chunk + 1) * p.chunk : no_limit;
 
     f32x16 o[4];  // O^T: [dim block], column = this lane's query
 #pragma unroll
@@ -332,18 +365,20 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
             }
 
         // ---- mask: keys past the segment end, and the chunk-causal rule.
+        // Positions increase with the key index, so the keys this lane's query
+        // sees in the tile are exactly j < lim (lane-local, 32-bit compare).
         // Register v of block kb holds key 32 kb + 8 (v/4) + 4 half + v%4.
-        const int64_t last_pos = pos0 + count - 1;
-        const bool full = count == BKV && (p.chunk <= 0 || last_pos / p.chunk <= r_first / p.chunk);
+        const bool full = count == BKV && pos0 + BKV <= wg_key_limit;
         if (!full) {
+            int64_t lim64 = key_limit - pos0;
+            lim64 = lim64 < count ? lim64 : count;
+            const int lim = lim64 < 0 ? 0 : (int)lim64;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    bool vis = j < count;
-                    if (p.chunk > 0) vis = vis && ((pos0 + j) / p.chunk <= qchunk);
-                    if (!vis) sacc[kb][v] = -INFINITY;
+                    if (j >= lim) sacc[kb][v] = -INFINITY;
                 }
         }
 
@@ -374,21 +409,20 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
         const float alpha = __builtin_amdgcn_exp2f(mrow - muse);
         mrow = mnew;
         float rs = 0.0f;
-        bf16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb, times the V scale
+        f16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                const float4 va = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 4 * half);
-                const float4 vb = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 8 + 4 * half);
-                const float vsc[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-                bf16x8 x;
+                float pv[8];
 #pragma unroll
                 for (int e2 = 0; e2 < 8; ++e2) {
-                    const float pv = __builtin_amdgcn_exp2f(sacc[kb][8 * tt + e2] - muse);
-                    rs += pv;
-                    x[e2] = (__bf16)(pv * vsc[e2]);
+                    pv[e2] = __builtin_amdgcn_exp2f(sacc[kb][8 * tt + e2] - muse);
+                    rs += pv[e2];
                 }
+                f16x8 x;
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) x[e2] = (_Float16)pv[e2];
                 pf[kb][tt] = x;
             }
         rs += __shfl_xor(rs, 32, 64);
@@ -410,8 +444,9 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
                 const int slice = kb * 2 + tt;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const bf16x8 vf = ld_bf16x8(vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2);
-                    o[db] = mfma_bf16(vf, pf[kb][tt], o[db]);
+                    const f16x8 vf = __builtin_bit_cast(
+                        f16x8, *reinterpret_cast<const uint4*>(vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2));
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kb][tt], o[db], 0, 0, 0);
                 }
             }
 

@@ -31,10 +31,16 @@ namespace gemm {
 
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int NT = 256;
+constexpr int GROUP_M = 8;
 constexpr int TILE_BYTES = BM * BK;         // one operand tile, 32 KB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // A + B
 
 enum Mode { ROWCOL = 0, BLOCKWISE = 1 };
+// Epilogue staging: each wave's 128 x 128 bf16 result, rows padded to 272 B so
+// the 16-byte row reads of the store pass are conflict-free.
+constexpr int OUT_ROW = 128 * 2 + 16;
+constexpr int OUT_WAVE_BYTES = 128 * OUT_ROW;
+constexpr int SMEM_BYTES = (4 * OUT_WAVE_BYTES > 2 * STAGE_BYTES) ? 4 * OUT_WAVE_BYTES : 2 * STAGE_BYTES;
 constexpr int kMaxKT = 256;  // K <= 32768
 
 struct Params {
@@ -47,15 +53,22 @@ struct Params {
     int64_t M, N, K, ldc;
     int act;
     int tiles_m, tiles_n;
+    int per_xcd;  // ceil(tiles / 8)
 };
 
-HN_DEVICE int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 4); }
+// 16-byte chunk c of LDS row r lives at chunk position c ^ ((r >> 1) & 7).
+// gfx950 serves a 16-byte LDS read 16 lanes at a time across 64 banks
+// (256 bytes): the 16 lanes of a fragment read hit 16 consecutive rows at one
+// logical chunk, and with 128-byte rows the bank group of (r, c) is
+// 8 (r & 1) + position, so the swizzle must spread rows of equal parity --
+// hence (r >> 1), not r.
+HN_DEVICE int swz_pos(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+HN_DEVICE int swz(int row, int chunk) { return row * BK + (swz_pos(row, chunk) << 4); }
 
 // Direct global -> LDS loads of one operand tile (global_load_lds_dwordx4:
 // 16 bytes per lane, written at M0 + 16 * lane). Each wave fills 8 regions of
 // 1 KB = 8 rows; a lane's bytes land at row lane / 8, physical chunk lane % 8,
-// so the lane fetches the logical chunk (lane % 8) ^ (row & 7) the swizzle
-// puts there. Rows past the operand's end are clamped to its last row: the
+// so the lane fetches the logical chunk the swizzle puts there. Rows past the operand's end are clamped to its last row: the
 // loads stay in bounds and the rows they fill are never stored.
 //
 // The load is issued from inline asm so the compiler does not track its LDS
@@ -83,7 +96,7 @@ HN_DEVICE void load_tile_lds(uint8_t* lds_tile, const uint8_t* __restrict__ base
     for (int i = 0; i < 8; ++i) {
         const int rgn = wave * 8 + i;
         const int r = rgn * 8 + (lane >> 3);
-        const int c = (lane & 7) ^ (lane >> 3);
+        const int c = swz_pos(r, lane & 7);  // the swizzle is an involution
         int64_t row = row0 + r;
         row = row < rows ? row : rows - 1;
         dma_16B(base + row * K + k0 + (c << 4),
@@ -108,25 +121,74 @@ HN_DEVICE f32x16 mfma(const i32x8& a, const i32x8& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// The eight fragments (4 weight blocks, 4 activation blocks) of one 64-byte
+// K slice of a stage, for the wave's 128 x 128 sub-tile.
+struct Frags {
+    i32x8 b[4];
+    i32x8 a[4];
+};
+
+HN_DEVICE void read_frags(Frags& f, const uint8_t* st, int kh, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.b[i] = read_frag(st + TILE_BYTES, wn * 128 + i * 32 + (lane & 31), kh, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.a[j] = read_frag(st, wm * 128 + j * 32 + (lane & 31), kh, lane);
+}
+
+HN_DEVICE void mfma_slice(f32x16 (&acc)[4][4], const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
+}
+
+// Interleave the 16 LDS reads of the next slice with this slice's 16 MFMAs.
+HN_DEVICE void interleave_reads_with_mfma() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    }
+}
+
 HN_DEVICE float gelu_tanh(float x) {
-    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh(u) = 1 - 2 / (e^{2u} + 1)
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    const float t = 1.0f - 2.0f / (__expf(2.0f * u) + 1.0f);
+    // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), with
+    // tanh(u) = 1 - 2 / (2^{2u log2 e} + 1) on v_exp_f32 / v_rcp_f32 (about
+    // 1 ulp each: far below the bf16 output's rounding). Saturates correctly:
+    // u -> +inf gives 1, u -> -inf gives -1.
+    const float u2 = x * fmaf(0.044715f * 2.0f * 0.7978845608028654f * 1.4426950408889634f, x * x,
+                              2.0f * 0.7978845608028654f * 1.4426950408889634f);
+    const float e = __builtin_amdgcn_exp2f(u2);
+    const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
     return 0.5f * x * (1.0f + t);
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+HN_DEVICE uint32_t pack_bf16(float a, float b) {
+    const f32x2_t f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 
 template <int MODE>
 __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
     // BLOCKWISE: the wave pair's scale rows, staged once so the K loop needs
     // no global scale loads: [2 m blocks][KT] then [2 n blocks][KT].
     __shared__ float sscale[4 * kMaxKT];
 
-    // Tile order: consecutive workgroups walk down M inside a column band of
-    // N so that the weight tile stays hot in L2 across neighbours.
-    const int tile = blockIdx.x;
-    const int tm = tile % p.tiles_m;
-    const int tn = tile / p.tiles_m;
+    // Tile order. Workgroup ids are dealt round-robin to the 8 XCDs, each with
+    // its own L2, so id % 8 selects a contiguous range of work items for that
+    // XCD. Work items are laid out in groups of GROUP_M tile rows, walking N
+    // inside a group: the ~32 tiles an XCD runs at once then cover GROUP_M
+    // activation tiles x 32/GROUP_M weight tiles, each fetched once into that
+    // L2 and reused by the other workgroups.
+    const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+    if (w >= p.tiles_m * p.tiles_n) return;
+    const int per_group = GROUP_M * p.tiles_n;
+    const int first_m = (w / per_group) * GROUP_M;
+    const int gm = min(GROUP_M, p.tiles_m - first_m);
+    const int tm = first_m + (w % per_group) % gm;
+    const int tn = (w % per_group) / gm;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const int lane = threadIdx.x & 63;
@@ -158,6 +220,44 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+    if (MODE == ROWCOL) {
+        // Software pipeline over K slices of 64 bytes (two per 128-byte stage).
+        // Phase A of step kt: MFMAs on slice 0 of stage kt while slice 1's
+        // fragments stream in from LDS. Then one wait + barrier: the DMA of
+        // stage kt+1 has landed and every wave is done reading stage kt, which
+        // immediately starts receiving step kt+2. Phase B: MFMAs on slice 1
+        // while slice 0 of stage kt+1 streams in.
+        uint8_t* const st0 = smem;
+        uint8_t* const st1 = smem + STAGE_BYTES;
+        load_tile_lds(st0, p.a, m0, p.M, p.K, 0, wave, lane);
+        load_tile_lds(st0 + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
+        if (KT > 1) {
+            load_tile_lds(st1, p.a, m0, p.M, p.K, BK, wave, lane);
+            load_tile_lds(st1 + TILE_BYTES, p.b, n0, p.N, p.K, BK, wave, lane);
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // stage 0 (issued first) landed
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        Frags f0, f1;
+        read_frags(f0, st0, 0, wm, wn, lane);
+        for (int kt = 0; kt < KT; ++kt) {
+            uint8_t* cur = (kt & 1) ? st1 : st0;
+            uint8_t* nxt = (kt & 1) ? st0 : st1;
+            read_frags(f1, cur, 1, wm, wn, lane);
+            mfma_slice(acc, f0);
+            interleave_reads_with_mfma();
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (kt + 2 < KT) {
+                load_tile_lds(cur, p.a, m0, p.M, p.K, (int64_t)(kt + 2) * BK, wave, lane);
+                load_tile_lds(cur + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 2) * BK, wave, lane);
+            }
+            if (kt + 1 < KT) read_frags(f0, nxt, 0, wm, wn, lane);
+            mfma_slice(acc, f1);
+            interleave_reads_with_mfma();
+        }
+    } else {
     load_tile_lds(smem, p.a, m0, p.M, p.K, 0, wave, lane);
     load_tile_lds(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
@@ -213,44 +313,62 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
+    }
 
-    // Epilogue. acc[i][j][v] holds out^T for n = n0 + wn*128 + 32 i + 8 (v/4)
-    // + 4 (lane/32) + v%4 and m = m0 + wm*128 + 32 j + lane%32.
+    // Epilogue. acc[i][j][v] holds out^T for n = wn*128 + 32 i + 8 (v/4) +
+    // 4 (lane/32) + v%4 and m = wm*128 + 32 j + lane%32 (tile-local). Each
+    // wave scales its 128 x 128 sub-tile, packs it to bf16 and parks it in its
+    // own LDS slice; then it writes the slice out as 256-byte row segments
+    // (16 lanes x 16 bytes per row, 4 rows per store).
+    __syncthreads();  // the last K step's LDS reads are done (all waves)
+    uint8_t* ow = smem + wave * OUT_WAVE_BYTES;
+    float sam[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-        if (m >= p.M) continue;
-        const float sam = MODE == ROWCOL ? p.sa[m] : 1.0f;
+        int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+        m = m < p.M ? m : p.M - 1;
+        sam[j] = MODE == ROWCOL ? p.sa[m] : 1.0f;
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int vq = 0; vq < 4; ++vq) {
-                const int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
-                if (n >= p.N) continue;
+        for (int vq = 0; vq < 4; ++vq) {
+            int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
+            n = n < p.N ? n : p.N - 4;  // stays in bounds; columns past N are not stored
+            float sbn[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (MODE == ROWCOL) {
+                const float4 s4 = *reinterpret_cast<const float4*>(p.sb + n);
+                sbn[0] = s4.x; sbn[1] = s4.y; sbn[2] = s4.z; sbn[3] = s4.w;
+                if (p.bias) {
+                    const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+                    bn[0] = bf16_bits_to_f32(bb.x & 0xffffu); bn[1] = bf16_bits_to_f32(bb.x >> 16);
+                    bn[2] = bf16_bits_to_f32(bb.y & 0xffffu); bn[3] = bf16_bits_to_f32(bb.y >> 16);
+                }
+            }
+            const int nl = i * 32 + vq * 8 + (lane >> 5) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
                 float y[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = acc[i][j][vq * 4 + e];
-                if (MODE == ROWCOL) {
-                    const float4 sbn = *reinterpret_cast<const float4*>(p.sb + n);
-                    y[0] *= sam * sbn.x; y[1] *= sam * sbn.y;
-                    y[2] *= sam * sbn.z; y[3] *= sam * sbn.w;
-                    if (p.bias) {
-                        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
-                        y[0] += bf16_bits_to_f32(bb.x & 0xffffu);
-                        y[1] += bf16_bits_to_f32(bb.x >> 16);
-                        y[2] += bf16_bits_to_f32(bb.y & 0xffffu);
-                        y[3] += bf16_bits_to_f32(bb.y >> 16);
-                    }
-                    if (p.act == HN_ACT_GELU_TANH) {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) y[e] = gelu_tanh(y[e]);
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = fmaf(acc[i][j][vq * 4 + e], sam[j] * sbn[e], bn[e]);
+                    if (MODE == ROWCOL && p.act == HN_ACT_GELU_TANH) y[e] = gelu_tanh(y[e]);
                 }
-                const uint32_t w0 = f32_to_bf16_bits(y[0]) | (f32_to_bf16_bits(y[1]) << 16);
-                const uint32_t w1 = f32_to_bf16_bits(y[2]) | (f32_to_bf16_bits(y[3]) << 16);
-                *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = make_uint2(w0, w1);
+                const int ml = j * 32 + (lane & 31);
+                *reinterpret_cast<uint2*>(ow + ml * OUT_ROW + nl * 2) =
+                    make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
             }
         }
+    // Each wave reads back only its own slice: no barrier needed beyond the
+    // wave's own LDS ordering.
+    __builtin_amdgcn_s_waitcnt(0);
+    const int64_t nbase = n0 + wn * 128 + (lane & 15) * 8;
+#pragma unroll 4
+    for (int r = 0; r < 32; ++r) {
+        const int ml = r * 4 + (lane >> 4);
+        const int64_t m = m0 + wm * 128 + ml;
+        const uint4 v = *reinterpret_cast<const uint4*>(ow + ml * OUT_ROW + (lane & 15) * 16);
+        if (m < p.M && nbase < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + nbase) = v;
     }
 }
 
@@ -281,7 +399,8 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     const int64_t tm = (M + gemm::BM - 1) / gemm::BM, tn = (N + gemm::BN - 1) / gemm::BN;
     HN_REQUIRE(tm * tn <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
     p.tiles_m = (int)tm; p.tiles_n = (int)tn;
-    const dim3 grid((unsigned)(tm * tn));
+    p.per_xcd = (int)((tm * tn + 7) / 8);
+    const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
     if (mode == gemm::ROWCOL)
         gemm::gemm_fp8_kernel<gemm::ROWCOL><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     else
