@@ -39,8 +39,10 @@ SIGNATURES = {
     "hn_gemm_fp8_rowcol": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
     "hn_gemm_fp8_blockwise": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "hn_attn_fp8kv": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P, _PI64,
-                      _I64, _P, _P, _PI64, _I64, _I64, _I64, _F, _P, _PI64, _P],
+                      _I64, _P, _P, _PI64, _I64, _I64, _I64, _F, _P, _PI64, _P, _I64, _P],
+    "hn_attn_fp8kv_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
 }
+RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64}
 
 _lib = None
 _lock = threading.Lock()
@@ -61,8 +63,7 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = _I
-        lib.hn_last_error.restype = ctypes.c_char_p
+            fn.restype = RESTYPES.get(name, _I)
         _lib = lib
         return lib
 

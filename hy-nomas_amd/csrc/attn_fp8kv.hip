@@ -9,13 +9,12 @@
 // through LDS in tiles of 64. K codes are widened to bf16 once per workgroup
 // as they are written to LDS (exact: every e4m3 and int8 code is a bf16
 // value) and the per-token K scale (times softmax_scale * log2 e) multiplies
-// the fp32 logits, so K enters as code * scale in fp32. V is dequantized once
-// per workgroup into fp16, fp16(code * scale) -- the value range of the
-// original activations, where fp16 keeps 11 significant bits -- and P stays in
-// [0, 1] as fp16, so the PV product carries 2^-11 relative rounding instead of
-// bf16's 2^-8. The optional unquantized tail (the current chunk's bf16 K/V) is
-// copied into the same LDS formats with unit K scales, so one compute path
-// serves both segments.
+// the fp32 logits, so K enters as code * scale in fp32. V codes are widened to
+// fp16 (also exact) and the per-token V scale multiplies the fp32 probability
+// before it is packed to fp16 for the PV MFMA: P' = fp16(p * s_v), so the PV
+// product carries fp16's 2^-11 relative rounding instead of bf16's 2^-8. The
+// optional unquantized tail (the current chunk's bf16 K/V) is copied into the
+// same LDS formats with unit scales, so one compute path serves both segments.
 //
 // Per tile the wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: the
 // MFMA output puts one query per lane column, so the online-softmax max/sum
@@ -43,10 +42,14 @@ constexpr int NT = 64 * NW;
 constexpr int QW = 32;             // queries per wave
 constexpr int BQ = QW * NW;        // queries per workgroup
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
-constexpr int VROW = BKV * 2 + 16; // V^T tile row: 64 fp16 + 16 B pad
+// V^T tile row: 64 fp16 + 8 B pad. 136 B = 34 dwords: rows 16 apart start
+// 32 banks apart (each V^T store instruction writes such a row pair, 2 x 128 B,
+// so it covers all 64 banks once), and 32 consecutive rows start on 32
+// distinct even banks (conflict-free 8-byte fragment reads).
+constexpr int VROW = BKV * 2 + 8;
 constexpr int K_BYTES = BKV * KROW;
 constexpr int V_BYTES = D * VROW;
-constexpr int S_BYTES = BKV * 4;  // per-key K scales (fp32)
+constexpr int S_BYTES = 2 * BKV * 4;  // per-key K and V scales (fp32)
 constexpr int STAGE = K_BYTES + V_BYTES + S_BYTES;
 
 struct Params {
@@ -67,8 +70,11 @@ struct Params {
     float scale_log2;  // softmax_scale * log2(e)
     int fmt;
     int q_tiles;       // ceil(Lq / BQ)
-    int work;          // B * H * q_tiles
+    int splits;        // key-range splits per (batch, head, query tile)
+    int work;          // B * H * q_tiles * splits
     int per_xcd;       // ceil(work / 8)
+    float* ws_o;       // splits > 1: unnormalized O, [split][B][H][Lq][D] fp32
+    float* ws_ml;      // splits > 1: running max and sum, [split][B][H][Lq][2]
 };
 
 // Position of key j (0..63) of a tile inside a V^T row: within each 16-key
@@ -82,8 +88,9 @@ HN_DEVICE int vpos(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); 
 // gfx950 conversion is used with a unit scale only: its scale operand applies
 // just the exponent of the fp32 value, so per-token scales are applied in fp32
 // by the caller instead.
-HN_DEVICE uint32_t cvt2(uint32_t w, bool hi, int fmt) {
-    if (fmt == HN_KV_FP8) {
+template <int FMT>
+HN_DEVICE uint32_t cvt2(uint32_t w, bool hi) {
+    if (FMT == HN_KV_FP8) {
         bf16x2 r = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
                       : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
         return __builtin_bit_cast(uint32_t, r);
@@ -95,12 +102,13 @@ HN_DEVICE uint32_t cvt2(uint32_t w, bool hi, int fmt) {
 }
 
 // 16 codes (one uint4) -> 16 bf16 as 8 dwords.
-HN_DEVICE void cvt16(const uint4& c, int fmt, uint32_t (&o)[8]) {
+template <int FMT>
+HN_DEVICE void cvt16(const uint4& c, uint32_t (&o)[8]) {
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        o[2 * i] = cvt2(w[i], false, fmt);
-        o[2 * i + 1] = cvt2(w[i], true, fmt);
+        o[2 * i] = cvt2<FMT>(w[i], false);
+        o[2 * i + 1] = cvt2<FMT>(w[i], true);
     }
 }
 
@@ -113,19 +121,18 @@ HN_DEVICE uint32_t pack_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
 }
 
-// 16 codes (one uint4) -> 16 fp16 of code * s (fp32 product, one RNE), 8 dwords.
-HN_DEVICE void dequant16_f16(const uint4& c, float s, int fmt, uint32_t (&o)[8]) {
+// 16 codes (one uint4) -> their 16 exact fp16 values, as 8 dwords.
+template <int FMT>
+HN_DEVICE void codes16_f16(const uint4& c, uint32_t (&o)[8]) {
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        if (fmt == HN_KV_FP8) {
-            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], false);
-            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[i], true);
-            o[2 * i] = pack_f16(lo.x * s, lo.y * s);
-            o[2 * i + 1] = pack_f16(hi.x * s, hi.y * s);
+        if (FMT == HN_KV_FP8) {
+            o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, false));
+            o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, true));
         } else {
-            o[2 * i] = pack_f16((float)(int8_t)(w[i] & 0xffu) * s, (float)(int8_t)((w[i] >> 8) & 0xffu) * s);
-            o[2 * i + 1] = pack_f16((float)(int8_t)((w[i] >> 16) & 0xffu) * s, (float)(int8_t)(w[i] >> 24) * s);
+            o[2 * i] = pack_f16((float)(int8_t)(w[i] & 0xffu), (float)(int8_t)((w[i] >> 8) & 0xffu));
+            o[2 * i + 1] = pack_f16((float)(int8_t)((w[i] >> 16) & 0xffu), (float)(int8_t)(w[i] >> 24));
         }
     }
 }
@@ -138,7 +145,8 @@ HN_DEVICE uint32_t bf16x2_to_f16x2(uint32_t w) {
 // Registers holding one cache tile between its global load and its LDS
 // write (the load is issued before the tile in LDS is consumed).
 // K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
-// V: thread t owns keys 2 (t / 8), +1 and 16 dims at 16 (t % 8).
+// V: lane l of wave w owns keys 2 (l % 32), +1 and the 16 dims of group
+//    2 w + l / 32, so one store instruction of a wave writes two whole V^T rows.
 struct CacheRegs {
     uint4 k[2];
     uint4 v[2];
@@ -157,7 +165,7 @@ HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t
         r.k[i] = *reinterpret_cast<const uint4*>(p.kc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (u & 7) * 16);
         r.sk[i] = p.ks[b * p.ss0 + tok * p.ss1 + h * p.ss2];
     }
-    const int kp = t >> 3, dg = t & 7;
+    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         int64_t j = kp * 2 + i;
@@ -171,7 +179,7 @@ HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t
 // V^T write of 2 consecutive keys x 16 dims: cv[key][e] holds dims (2e, 2e+1).
 HN_DEVICE void store_vt(uint8_t* vl, const uint32_t (&cv)[2][8]) {
     const int t = threadIdx.x;
-    const int kp = t >> 3, dg = t & 7;
+    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
     const int pos = vpos(kp * 2);  // the pair stays adjacent: vpos keeps bits 0-1
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -183,9 +191,10 @@ HN_DEVICE void store_vt(uint8_t* vl, const uint32_t (&cv)[2][8]) {
     }
 }
 
-// Per-key scales in LDS: K scale * softmax_scale * log2 e.
+// Per-key scales in LDS: [0, 64) K scale * softmax_scale * log2 e, [64, 128) V scale.
 HN_DEVICE float* stage_scales(uint8_t* st) { return reinterpret_cast<float*>(st + K_BYTES + V_BYTES); }
 
+template <int FMT>
 HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st) {
     const int t = threadIdx.x;
     float* sc = stage_scales(st);
@@ -193,7 +202,7 @@ HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st
     for (int i = 0; i < 2; ++i) {
         const int u = t + NT * i;
         uint32_t o[8];
-        cvt16(r.k[i], p.fmt, o);
+        cvt16<FMT>(r.k[i], o);
         uint4* dst = reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32);
         dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
         dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -201,8 +210,12 @@ HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st
     }
     uint32_t cv[2][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dequant16_f16(r.v[i], r.sv[i], p.fmt, cv[i]);
+    for (int i = 0; i < 2; ++i) codes16_f16<FMT>(r.v[i], cv[i]);
     store_vt(st + K_BYTES, cv);
+    if (t < 32) {  // dim group 0: lane t holds keys 2 t, 2 t + 1
+        sc[BKV + t * 2] = r.sv[0];
+        sc[BKV + t * 2 + 1] = r.sv[1];
+    }
 }
 
 // Unquantized tail tile (bf16 K/V of the current chunk): load and write to LDS
@@ -222,7 +235,7 @@ HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t fir
         dst[0] = lo;
         dst[1] = hi;
     }
-    const int kp = t >> 3, dg = t & 7;
+    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
     uint32_t cv[2][8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -238,6 +251,7 @@ HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t fir
     store_vt(st + K_BYTES, cv);
     float* sc = stage_scales(st);
     if (t < BKV) sc[t] = p.scale_log2;
+    else if (t < 2 * BKV) sc[t] = 1.0f;
 }
 
 HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -248,6 +262,7 @@ HN_DEVICE bf16x8 ld_bf16x8(const uint8_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
+template <int FMT>
 __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
 
@@ -257,9 +272,11 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     const int id = blockIdx.x;
     const int w = (id & 7) * p.per_xcd + (id >> 3);
     if (w >= p.work) return;
-    const int qt = w % p.q_tiles;
-    const int64_t h = (w / p.q_tiles) % p.H;
-    const int64_t b = w / (p.q_tiles * (int)p.H);
+    const int split = w % p.splits;
+    const int wq = w / p.splits;
+    const int qt = wq % p.q_tiles;
+    const int64_t h = (wq / p.q_tiles) % p.H;
+    const int64_t b = wq / (p.q_tiles * (int)p.H);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -294,7 +311,10 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     const int64_t tail_end = pos_end - p.kv_len;  // tail keys visited (may be <= 0)
     const int n_cache = (int)((cache_end + BKV - 1) / BKV);
     const int n_tail = tail_end > 0 ? (int)((tail_end + BKV - 1) / BKV) : 0;
-    const int n_tiles = n_cache + n_tail;
+    const int n_all = n_cache + n_tail;
+    // This split's share of the tile list [t_begin, t_end).
+    const int t_begin = (int)((int64_t)n_all * split / p.splits);
+    const int t_end = (int)((int64_t)n_all * (split + 1) / p.splits);
     // Visibility limits (exclusive key positions): this lane's query, and the
     // workgroup's first query (every key below it is visible to all lanes).
     const int64_t no_limit = p.kv_len + p.cur_len;
@@ -325,27 +345,27 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
         count = count < BKV ? count : BKV;
     };
 
-    if (n_tiles > 0) {
+    if (t_end > t_begin) {
         bool cs;
         int64_t first, count, pos0;
-        tile_geom(0, cs, first, count, pos0);
+        tile_geom(t_begin, cs, first, count, pos0);
         if (cs) {
             load_cache_tile(p, regs, b, h, first, count);
-            store_cache_tile(p, regs, smem);
+            store_cache_tile<FMT>(p, regs, smem);
         } else {
             copy_tail_tile(p, b, h, first, count, smem);
         }
     }
     __syncthreads();
 
-    for (int t = 0; t < n_tiles; ++t) {
-        const uint8_t* st = smem + (t & 1) * STAGE;
+    for (int t = t_begin; t < t_end; ++t) {
+        const uint8_t* st = smem + ((t - t_begin) & 1) * STAGE;
         bool cs;
         int64_t first, count, pos0;
         tile_geom(t, cs, first, count, pos0);
         bool ncs = false;
         int64_t nf = 0, nc = 0, np = 0;
-        if (t + 1 < n_tiles) {
+        if (t + 1 < t_end) {
             tile_geom(t + 1, ncs, nf, nc, np);
             if (ncs) load_cache_tile(p, regs, b, h, nf, nc);
         }
@@ -409,11 +429,16 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
         const float alpha = __builtin_amdgcn_exp2f(mrow - muse);
         mrow = mnew;
         float rs = 0.0f;
-        f16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb
+        f16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb, times the V scale
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
+                // registers 8t .. 8t+3 hold keys 32 kb + 16 t + 4 half + 0..3,
+                // registers 8t+4 .. 8t+7 keys 32 kb + 16 t + 8 + 4 half + 0..3
+                const float4 va = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 4 * half);
+                const float4 vb = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 8 + 4 * half);
+                const float vsc[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
                 float pv[8];
 #pragma unroll
                 for (int e2 = 0; e2 < 8; ++e2) {
@@ -422,7 +447,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
                 }
                 f16x8 x;
 #pragma unroll
-                for (int e2 = 0; e2 < 8; ++e2) x[e2] = (_Float16)pv[e2];
+                for (int e2 = 0; e2 < 8; ++e2) x[e2] = (_Float16)(pv[e2] * vsc[e2]);
                 pf[kb][tt] = x;
             }
         rs += __shfl_xor(rs, 32, 64);
@@ -444,21 +469,40 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
                 const int slice = kb * 2 + tt;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const f16x8 vf = __builtin_bit_cast(
-                        f16x8, *reinterpret_cast<const uint4*>(vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2));
+                    const uint8_t* vp = vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2;
+                    const uint2 v0 = *reinterpret_cast<const uint2*>(vp);
+                    const uint2 v1 = *reinterpret_cast<const uint2*>(vp + 8);
+                    const f16x8 vf = __builtin_bit_cast(f16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kb][tt], o[db], 0, 0, 0);
                 }
             }
 
-        if (t + 1 < n_tiles) {
-            uint8_t* nst = smem + ((t + 1) & 1) * STAGE;
-            if (ncs) store_cache_tile(p, regs, nst);
+        if (t + 1 < t_end) {
+            uint8_t* nst = smem + ((t + 1 - t_begin) & 1) * STAGE;
+            if (ncs) store_cache_tile<FMT>(p, regs, nst);
             else copy_tail_tile(p, b, h, nf, nc, nst);
         }
         __syncthreads();
     }
 
     // ---- epilogue: O = O^T / l; the lane holds dims 32 db + 8 (v/4) + 4 half + v%4
+    if (p.splits > 1) {
+        // Unnormalized partial result of this key range, merged by attn_combine_kernel.
+        if (qvalid) {
+            const int64_t qi = ((((int64_t)split * (p.work / p.splits / p.q_tiles / p.H)) + b) * p.H + h) * p.Lq + row;
+            float* dst = p.ws_o + qi * D;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int vq = 0; vq < 4; ++vq) {
+                    const int d = db * 32 + vq * 8 + half * 4;
+                    *reinterpret_cast<float4*>(dst + d) =
+                        make_float4(o[db][vq * 4], o[db][vq * 4 + 1], o[db][vq * 4 + 2], o[db][vq * 4 + 3]);
+                }
+            if (half == 0) *reinterpret_cast<float2*>(p.ws_ml + qi * 2) = make_float2(mrow, lsum);
+        }
+        return;
+    }
     if (qvalid) {
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         uint16_t* dst = p.out + b * p.os0 + row * p.os1 + h * p.os2;
@@ -476,10 +520,63 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     }
 }
 
+// Merge of the per-split partial results: with M = max_s m_s,
+// O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (0 when no key was visible).
+// One 128-thread block per (batch, head, query); thread d owns one dimension.
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ ws_o,
+                                                           const float* __restrict__ ws_ml,
+                                                           int splits, int64_t rows_per_split,
+                                                           int64_t Lq, int64_t H, uint16_t* out,
+                                                           int64_t os0, int64_t os1, int64_t os2) {
+    const int64_t r = blockIdx.x;  // (b * H + h) * Lq + q
+    const int d = threadIdx.x;
+    float M = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ws_ml[(sp * rows_per_split + r) * 2]);
+    const float Muse = M == -INFINITY ? 0.0f : M;
+    float num = 0.0f, den = 0.0f;
+    for (int sp = 0; sp < splits; ++sp) {
+        const int64_t idx = sp * rows_per_split + r;
+        const float wgt = __builtin_amdgcn_exp2f(ws_ml[idx * 2] - Muse);
+        den = fmaf(wgt, ws_ml[idx * 2 + 1], den);
+        num = fmaf(wgt, ws_o[idx * D + d], num);
+    }
+    const int64_t q = r % Lq, h = (r / Lq) % H, b = r / (Lq * H);
+    out[b * os0 + q * os1 + h * os2 + d] = (uint16_t)f32_to_bf16_bits(den > 0.0f ? num / den : 0.0f);
+}
+
 }  // namespace attn
 }  // namespace hn
 
 using namespace hn;
+
+// Split selection: a launch wants at least two workgroups per CU (two fit per
+// CU by LDS and registers). When (batch x heads x query tiles) falls short, the
+// key range of each query tile is split so that the grid fills the device
+// (the decode-style case: a few hundred queries over a long cache); each split
+// keeps at least 16 key tiles.
+static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t cur_len) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    const int64_t work = B * H * ((Lq + attn::BQ - 1) / attn::BQ);
+    const int64_t target = 2LL * cus;
+    if (work <= 0 || work >= target) return 1;
+    const int64_t tiles = (kv_len + cur_len + attn::BKV - 1) / attn::BKV;
+    int64_t sp = (target + work - 1) / work;
+    const int64_t cap = tiles / 16;
+    if (sp > cap) sp = cap;
+    return sp > 1 ? (int)sp : 1;
+}
+
+extern "C" int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                                int64_t kv_len, int64_t cur_len) {
+    if (B <= 0 || Lq <= 0 || H <= 0 || D != attn::D || kv_len < 0 || cur_len < 0) return 0;
+    const int sp = attn_splits(B, Lq, H, kv_len, cur_len);
+    if (sp <= 1) return 0;
+    return (int64_t)sp * B * H * Lq * (D + 2) * (int64_t)sizeof(float);
+}
 
 extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
                              int64_t H, int64_t D, const void* kc, const void* vc,
@@ -487,7 +584,8 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
                              const int64_t* ss, int64_t kv_len, const void* kcur,
                              const void* vcur, const int64_t* curs, int64_t cur_len,
                              int64_t q_pos0, int64_t chunk_len, float softmax_scale, void* out,
-                             const int64_t* os, void* stream) {
+                             const int64_t* os, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
     HN_REQUIRE(fmt == HN_KV_FP8 || fmt == HN_KV_INT8, HN_E_ARG, "hn_attn_fp8kv: unknown KV format");
     HN_REQUIRE(D == attn::D, HN_E_ARG, "hn_attn_fp8kv: head dim must be 128");
     HN_REQUIRE(B >= 0 && Lq >= 0 && H > 0 && kv_len >= 0 && cur_len >= 0 && q_pos0 >= 0, HN_E_ARG,
@@ -537,12 +635,28 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
     p.scale_log2 = softmax_scale * 1.4426950408889634f;
     p.fmt = fmt;
     const int64_t qt = (Lq + attn::BQ - 1) / attn::BQ;
-    const int64_t work = B * H * qt;
+    const int sp = attn_splits(B, Lq, H, kv_len, cur_len);
+    const int64_t need = sp > 1 ? (int64_t)sp * B * H * Lq * (D + 2) * (int64_t)sizeof(float) : 0;
+    HN_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))), HN_E_ARG,
+               "hn_attn_fp8kv: workspace smaller than hn_attn_fp8kv_workspace_size() or misaligned");
+    const int64_t work = B * H * qt * sp;
     HN_REQUIRE(work <= 0x3fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too much work for one launch");
     p.q_tiles = (int)qt;
+    p.splits = sp;
     p.work = (int)work;
     p.per_xcd = (int)((work + 7) / 8);
+    p.ws_o = sp > 1 ? (float*)workspace : nullptr;
+    p.ws_ml = sp > 1 ? (float*)workspace + (int64_t)sp * B * H * Lq * D : nullptr;
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    attn::attn_fp8kv_kernel<<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
-    return check_launch("hn_attn_fp8kv");
+    if (fmt == HN_KV_FP8)
+        attn::attn_fp8kv_kernel<HN_KV_FP8><<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
+    else
+        attn::attn_fp8kv_kernel<HN_KV_INT8><<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
+    int rc = check_launch("hn_attn_fp8kv");
+    if (rc != HN_OK || sp <= 1) return rc;
+    const int64_t rows = B * H * Lq;
+    HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too many rows to combine");
+    attn::attn_combine_kernel<<<(unsigned)rows, attn::D, 0, (hipStream_t)stream>>>(
+        p.ws_o, p.ws_ml, sp, rows, Lq, H, (uint16_t*)out, os[0], os[1], os[2]);
+    return check_launch("hn_attn_fp8kv (combine)");
 }

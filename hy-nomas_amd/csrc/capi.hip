@@ -19,4 +19,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* hn_last_error(void) { return hn::g_last_error; }
 
-extern "C" int hn_abi_version(void) { return 1; }
+extern "C" int hn_abi_version(void) { return 2; }

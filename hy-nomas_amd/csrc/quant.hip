@@ -11,6 +11,19 @@
 
 namespace hn {
 
+// Eight bf16 (one uint4) -> eight e4m3 codes of x / s (IEEE fp32 division,
+// then RNE to e4m3), as two dwords.
+HN_DEVICE uint2 encode8(const uint4& v, float s) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_bits_to_f32(w[j] & 0xffffu) / s;
+        f[2 * j + 1] = bf16_bits_to_f32(w[j] >> 16) / s;
+    }
+    return make_uint2(e4m3_encode4(f[0], f[1], f[2], f[3]), e4m3_encode4(f[4], f[5], f[6], f[7]));
+}
+
 // ---------------------------------------------------------------------------
 // Per-row quantization. One 256-thread block per row; each thread keeps up to
 // CPT chunks of 8 bf16 in registers between the amax pass and the encode pass,
@@ -50,16 +63,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     for (int i = 0; i < CPT; ++i) {
         const int c = threadIdx.x + i * 256;
         if (c < nchunks) {
-            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-            uint32_t lo = 0, hi = 0;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                lo |= e4m3_encode(bf16_bits_to_f32(w[j] & 0xffffu) / s) << (16 * j);
-                lo |= e4m3_encode(bf16_bits_to_f32(w[j] >> 16) / s) << (16 * j + 8);
-                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] & 0xffffu) / s) << (16 * j);
-                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] >> 16) / s) << (16 * j + 8);
-            }
-            *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8(v[i], s);
         }
     }
 }
@@ -103,16 +107,7 @@ __global__ __launch_bounds__(256) void quantize_blockwise_kernel(
         const int64_t r = r0 + (id >> 4);
         const int64_t c = c0 + (id & 15) * 8;
         if (r < rows) {
-            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-            uint32_t lo = 0, hi = 0;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                lo |= e4m3_encode(bf16_bits_to_f32(w[j] & 0xffffu) / s) << (16 * j);
-                lo |= e4m3_encode(bf16_bits_to_f32(w[j] >> 16) / s) << (16 * j + 8);
-                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] & 0xffffu) / s) << (16 * j);
-                hi |= e4m3_encode(bf16_bits_to_f32(w[j + 2] >> 16) / s) << (16 * j + 8);
-            }
-            *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(q + r * cols + c) = encode8(v[i], s);
         }
     }
 }
@@ -141,42 +136,59 @@ HN_DEVICE uint32_t int8_code(float v) {
     return (uint32_t)(int32_t)r & 0xffu;
 }
 
+constexpr int KV_ROWS_PER_GROUP = 4;  // rows each 16-lane group carries (loads issued together)
+
 template <int FMT>
 __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
     const int sel = blockIdx.y;
-    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    if (row >= a.rows) return;
     const int lane16 = threadIdx.x & 15;
-    const int64_t h = row % a.H;
-    const int64_t t = (row / a.H) % a.L;
-    const int64_t b = row / (a.H * a.L);
-    const uint4 v = *reinterpret_cast<const uint4*>(a.x[sel] + b * a.xs0 + t * a.xs1 +
-                                                    h * a.xs2 + lane16 * 8);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    float f[8];
+    // The 16 groups of a block take interleaved rows so that, for each of the
+    // KV_ROWS_PER_GROUP steps, the block covers 16 consecutive rows.
+    const int64_t base = (int64_t)blockIdx.x * 16 * KV_ROWS_PER_GROUP + (threadIdx.x >> 4);
+    uint4 v[KV_ROWS_PER_GROUP];
+    int64_t rb[KV_ROWS_PER_GROUP], rt[KV_ROWS_PER_GROUP], rh[KV_ROWS_PER_GROUP];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        f[2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
-        f[2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+    for (int k = 0; k < KV_ROWS_PER_GROUP; ++k) {
+        int64_t row = base + k * 16;
+        row = row < a.rows ? row : a.rows - 1;  // duplicates of the last row rewrite identical bytes
+        rh[k] = row % a.H;
+        rt[k] = (row / a.H) % a.L;
+        rb[k] = row / (a.H * a.L);
+        v[k] = *reinterpret_cast<const uint4*>(a.x[sel] + rb[k] * a.xs0 + rt[k] * a.xs1 +
+                                               rh[k] * a.xs2 + lane16 * 8);
     }
-    float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
-    amax = group_max<16>(amax);
-    const float qmax = FMT == HN_KV_FP8 ? kE4M3Max : 127.0f;
-    const float s = amax > 0.0f ? amax / qmax : 1.0f;
-    uint32_t lo = 0, hi = 0;
+    for (int k = 0; k < KV_ROWS_PER_GROUP; ++k) {
+        const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+        float f[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c0 = FMT == HN_KV_FP8 ? e4m3_encode(f[j] / s) : int8_code(f[j] / s);
-        const uint32_t c1 = FMT == HN_KV_FP8 ? e4m3_encode(f[j + 4] / s) : int8_code(f[j + 4] / s);
-        lo |= c0 << (8 * j);
-        hi |= c1 << (8 * j);
+        for (int j = 0; j < 4; ++j) {
+            f[2 * j] = bf16_bits_to_f32(w[j] & 0xffffu);
+            f[2 * j + 1] = bf16_bits_to_f32(w[j] >> 16);
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(f[j]));
+        amax = group_max<16>(amax);
+        const float qmax = FMT == HN_KV_FP8 ? kE4M3Max : 127.0f;
+        const float s = amax > 0.0f ? amax / qmax : 1.0f;
+        uint32_t lo, hi;
+        if (FMT == HN_KV_FP8) {
+            lo = e4m3_encode4(f[0] / s, f[1] / s, f[2] / s, f[3] / s);
+            hi = e4m3_encode4(f[4] / s, f[5] / s, f[6] / s, f[7] / s);
+        } else {
+            lo = hi = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo |= int8_code(f[j] / s) << (8 * j);
+                hi |= int8_code(f[j + 4] / s) << (8 * j);
+            }
+        }
+        const int64_t tt = rt[k] + a.start;
+        *reinterpret_cast<uint2*>(a.q[sel] + rb[k] * a.qs0 + tt * a.qs1 + rh[k] * a.qs2 + lane16 * 8) =
+            make_uint2(lo, hi);
+        if (lane16 == 0) a.s[sel][rb[k] * a.ss0 + tt * a.ss1 + rh[k] * a.ss2] = s;
     }
-    const int64_t tt = t + a.start;
-    *reinterpret_cast<uint2*>(a.q[sel] + b * a.qs0 + tt * a.qs1 + h * a.qs2 + lane16 * 8) =
-        make_uint2(lo, hi);
-    if (lane16 == 0) a.s[sel][b * a.ss0 + tt * a.ss1 + h * a.ss2] = s;
 }
 
 // KV decode of a valid prefix into bf16: y = bf16_rne(decode(q) * s).
@@ -312,7 +324,7 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
     a.qs0 = qs[0]; a.qs1 = qs[1]; a.qs2 = qs[2];
     a.ss0 = ss[0]; a.ss1 = ss[1]; a.ss2 = ss[2];
     a.L = L; a.H = H; a.rows = rows; a.start = start;
-    const int64_t blocks = (rows + 15) / 16;
+    const int64_t blocks = (rows + 16 * KV_ROWS_PER_GROUP - 1) / (16 * KV_ROWS_PER_GROUP);
     HN_REQUIRE(blocks <= 0x7fffffffLL, HN_E_ARG, "KV write too large");
     const dim3 grid((unsigned)blocks, (unsigned)n);
     if (fmt == HN_KV_FP8)

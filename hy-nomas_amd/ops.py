@@ -263,13 +263,17 @@ def attn_fp8kv(q: torch.Tensor, k_codes: torch.Tensor, v_codes: torch.Tensor,
                     or k_cur.dtype != torch.bfloat16 or v_cur.dtype != torch.bfloat16):
         raise ValueError("k_cur/v_cur must be matching bf16 tensors")
     with torch.cuda.device(q.device):
-        L.check(L.load().hn_attn_fp8kv(
+        lib = L.load()
+        ws_bytes = lib.hn_attn_fp8kv_workspace_size(B, Lq, H, D, kv_len, cur_len)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device) if ws_bytes else None
+        L.check(lib.hn_attn_fp8kv(
             fmt, q.data_ptr(), L.strides(q), B, Lq, H, D,
             k_codes.data_ptr(), v_codes.data_ptr(), L.strides(k_codes),
             k_scale.data_ptr(), v_scale.data_ptr(), L.strides(k_scale), kv_len,
             None if not cur_len else k_cur.data_ptr(), None if not cur_len else v_cur.data_ptr(),
             L.strides(k_cur) if cur_len else None, cur_len, q_pos0, chunk_len,
-            float(softmax_scale), out.data_ptr(), L.strides(out), _stream(q)), "hn_attn_fp8kv")
+            float(softmax_scale), out.data_ptr(), L.strides(out),
+            None if ws is None else ws.data_ptr(), ws_bytes, _stream(q)), "hn_attn_fp8kv")
     return out
 
 

@@ -139,6 +139,11 @@ int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const f
  *   out:   bf16 [B, Lq, H, D], strides os[4]
  * O = softmax(Q K^T * softmax_scale) V with K, V dequantized as code * scale;
  * query rows that see no key are written as zeros.
+ * workspace: device scratch of at least hn_attn_fp8kv_workspace_size(...)
+ *        bytes (16-byte aligned; NULL/0 when that size is 0). It holds per-split
+ *        partial results when the key range is split across workgroups to fill
+ *        the device (few queries, long cache); concurrent calls need separate
+ *        workspaces.
  * Replaces the FP8/INT8-cache branch of causal_attention_with_cache_mp,
  * hymm/models/dit/nomas_cpt.py:529-531,614-625,771-829 (dequantize_kv, cat,
  * then Flex/FA3/SDPA), and flex_masked_attention, range_attention.py:212-239. */
@@ -147,7 +152,12 @@ int hn_attn_fp8kv(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t 
                   const float *ks, const float *vs, const int64_t *ss, int64_t kv_len,
                   const void *kcur, const void *vcur, const int64_t *curs, int64_t cur_len,
                   int64_t q_pos0, int64_t chunk_len, float softmax_scale, void *out,
-                  const int64_t *os, void *stream);
+                  const int64_t *os, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Bytes of workspace hn_attn_fp8kv needs for these sizes on the current device
+ * (0: none). Depends on the device's CU count. */
+int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
+                                     int64_t kv_len, int64_t cur_len);
 
 #ifdef __cplusplus
 }

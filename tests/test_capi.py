@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.hn_abi_version() == 1
+    assert lib.hn_abi_version() == 2
 
 
 def _err(lib):
@@ -56,8 +56,9 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert "activation" in _err(lib)
     assert lib.hn_gemm_fp8_blockwise(None, None, None, None, None, 16, 128, 96, None) == -1
     assert lib.hn_attn_fp8kv(0, None, st, 1, 1, 1, 64, None, None, st, None, None, st, 0,
-                             None, None, None, 0, 0, 0, 1.0, None, st, None) == -1
+                             None, None, None, 0, 0, 0, 1.0, None, st, None, 0, None) == -1
     assert "head dim" in _err(lib)
+    assert lib.hn_attn_fp8kv_workspace_size(1, 128, 24, 64, 1000, 0) == 0   # bad head dim
     # zero-size work is a no-op that needs no pointers
     assert lib.hn_quantize_rows_fp8(None, 0, 8, 8, 0, 1e-4, None, None, None) == L.HN_OK
     assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 0, 128, 128, 128, 0, None) == L.HN_OK

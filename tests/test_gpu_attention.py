@@ -113,6 +113,25 @@ def test_chunk_attention_two_chunk_queries_triangle(O, dev):
     assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="triangle")
 
 
+@pytest.mark.parametrize("Lq,kv_len,H", [(128, 86400, 24), (100, 20000, 4), (1, 5000, 2)])
+def test_split_kv_decode_style(O, dev, Lq, kv_len, H):
+    """Few queries over a long cache: the key range is split across workgroups
+    (workspace + combine); rows checked against the oracle."""
+    print(f"case split-kv Lq={Lq} kv={kv_len} H={H}", flush=True)
+    lib = pkg_module("_lib").load()
+    assert lib.hn_attn_fp8kv_workspace_size(1, Lq, H, 128, kv_len, 0) > 0
+    ca = pkg_module("cache_attention")
+    chunk = kv_len // 8 if kv_len % 8 == 0 else kv_len
+    n = kv_len // chunk
+    cache = _cache_from_chunks(dev, n, chunk, H, 128, 300 + Lq)
+    q = _q(dev, Lq, H, 128, 11)
+    out = ca.chunk_attention(q, cache, kv_len)
+    rows = np.arange(0, Lq, max(1, Lq // 16))
+    kh, vh = _dequant(O, cache, kv_len)
+    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh)
+    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="split-kv")
+
+
 def test_attention_invariants(dev):
     """Constant V -> O = V; no visible key -> zeros."""
     kvc = pkg_module("fp8_kv_cache")
