@@ -11,6 +11,9 @@ ms / GB/s and the KV-write GB/s ride along in the same JSON line, as does the
 config-1 linear. Timing uses HIP events on the stream the kernels run on.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--only all|linear|kv|attn|copy]
+``--only`` runs one workload (for per-kernel counter passes); ``copy`` is a
+plain 1 GiB device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
 """
 from __future__ import annotations
 
@@ -76,6 +79,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "copy"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -92,6 +96,15 @@ def main():
 
     def log(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        ms = time_loop(lambda: dst.copy_(src), args.steps, args.warmup)
+        log(f"copy 1 GiB: {ms:.3f} ms ({2 * (1 << 30) / (ms * 1e-3) / 1e9:.0f} GB/s read+write)")
+        return
+    if args.only != "all":
+        return run_only(args, torch, ops, kvc, ca, dev, log)
 
     # ---------------- FP8 linear, north-star shape
     g = torch.Generator(device=dev).manual_seed(1234)
@@ -187,7 +200,7 @@ def main():
             "peak": FP8_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": gemm_traffic_bytes(),
         },
         "linear": {"ms": round(ms_linear, 4), "tflops": round(linear_tflops, 2),
                    "frac_fp8_peak": round(linear_tflops / FP8_PEAK_TFLOPS, 4),
@@ -206,6 +219,47 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+def run_only(args, torch, ops, kvc, ca, dev, log):
+    """One workload, for per-kernel counter passes (no JSON line)."""
+    g = torch.Generator(device=dev).manual_seed(1234)
+    if args.only == "linear":
+        x = torch.randn(NS_M, NS_K, device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn(NS_N, NS_K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        bias = torch.zeros(NS_N, device=dev, dtype=torch.bfloat16)
+        qw, sw = ops.quantize_rows_fp8(w)
+        qx, sx = ops.quantize_rows_fp8(x)
+        ms = time_loop(lambda: ops.gemm_fp8_rowcol(qx, qw, sx, sw, bias, 1), args.steps, args.warmup)
+        log(f"north-star GEMM {ms:.3f} ms")
+    elif args.only == "kv":
+        k = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+        cache = kvc.make_fp8_kv_block(1, KV_L, KV_H, KV_D, device=dev)
+        ms = time_loop(lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"],
+                                                     cache["v_scale"], k, k, 0), args.steps, args.warmup)
+        log(f"KV write {ms * 1e3:.1f} us")
+    elif args.only == "attn":
+        lk = ATT_CHUNKS * KV_L
+        cache = kvc.make_fp8_kv_block(1, lk, KV_H, KV_D, device=dev)
+        for c in range(ATT_CHUNKS):
+            kc = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+            kvc.quantize_kv_pair_into(cache, kc, kc, c * KV_L)
+        q = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+        ms = time_loop(lambda: ca.chunk_attention(q, cache, lk, q_pos0=lk - KV_L, chunk_len=KV_L),
+                       args.steps, args.warmup)
+        log(f"chunk attention {ms:.3f} ms")
+
+
+def gemm_traffic_bytes():
+    """HBM bytes per north-star GEMM launch from the committed counter summary
+    (profiles/fp8_gemm_north_star_traffic.json), or None."""
+    f = ROOT / "profiles" / "fp8_gemm_north_star_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
 
 
 def cpu_baseline(seconds, log):
