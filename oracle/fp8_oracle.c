@@ -10,7 +10,7 @@
  * FMA contraction, so every float operation is one IEEE-754 binary32 op exactly
  * as ATen's CPU kernels perform it).
  *
- * Parity pins (see tests/test_oracle_*.py):
+ * Parity pins (tests/test_oracle.py):
  *   - e4m3 encode: exhaustive over all 2^16 bf16 bit patterns and a large
  *     random sample of fp32 patterns against torch's float8_e4m3fn cast,
  *     plus hand-derived known answers (448 -> 0x7E, 464 tie -> 0x7E,
