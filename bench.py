@@ -169,6 +169,10 @@ def main():
     dec_gbs = attn_unique_bytes(KV_H, 128, lk, KV_D) / (ms_dec * 1e-3) / 1e9
     log(f"decode-style attention (Lq=128) {ms_dec * 1e3:.1f} us ({dec_gbs:.0f} GB/s)")
 
+    # ---------------- config 4: one FP8 DiT block over 7 cached chunks + the current one
+    blk_res = bench_block(args, torch, cache, dev, g, log)
+    del cache, q, qd
+
     # ---------------- CPU baseline: the oracle's dequantize-then-matmul
     cpu = None
     if not args.no_cpu_baseline:
@@ -216,9 +220,40 @@ def main():
                       "decode_lq128_us": round(ms_dec * 1e3, 2),
                       "decode_lq128_gbs": round(dec_gbs, 1),
                       "decode_frac_hbm": round(dec_gbs / HBM_PEAK_GBS, 4)},
+        "dit_block": blk_res,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+def block_flops(hidden=3072, heads=24, tokens=KV_L, keys=ATT_CHUNKS * KV_L, d=KV_D, mlp=4):
+    """Linears (QKV, out-proj, fc1, fc2) + attention over ``keys`` keys."""
+    lin = 2.0 * tokens * hidden * (3 * hidden + hidden + 2 * mlp * hidden)
+    return lin, attn_flops(heads, tokens, keys, d)
+
+
+def bench_block(args, torch, cache, dev, g, log):
+    """Config 4: one block's image stream, FP8 linears, attention over the FP8
+    cache's first 7 chunks plus the current chunk as a bf16 tail."""
+    db = importlib.import_module("hy-nomas_amd.dit_block")
+    metrics = importlib.import_module("hy-nomas_amd.metrics")
+    hist = (ATT_CHUNKS - 1) * KV_L
+    blk = db.FP8DiTBlock(3072, KV_H, device=dev, generator=g)
+    img = torch.randn(1, KV_L, 3072, device=dev, generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, 3072, device=dev, generator=g).to(torch.bfloat16)
+    cos, sin = db.rope_tables(3, 45, 80, t_offset=3 * (ATT_CHUNKS - 1), device=dev)
+    fn = lambda: blk(img, vec, cos, sin, cache, hist, update_cache=False)
+    with torch.no_grad():
+        ms = time_loop(fn, max(2, args.steps // 4), max(1, args.warmup // 2))
+        with metrics.StageMetrics() as m:
+            fn()
+    lin, att = block_flops()
+    tflops = (lin + att) / (ms * 1e-3) / 1e12
+    stages = {k: round(v["seconds"] * 1e3, 3) for k, v in m.summary().items()}
+    log(f"config-4 block {ms:.3f} ms ({tflops:.0f} TFLOP/s); stages (synchronized) ms {stages}")
+    return {"ms": round(ms, 4), "tflops": round(tflops, 2), "linear_tflop": round(lin / 1e12, 4),
+            "attention_tflop": round(att / 1e12, 4), "stage_ms": stages,
+            "shape": {"tokens": KV_L, "hidden": 3072, "heads": KV_H, "cached_tokens": hist}}
 
 
 def run_only(args, torch, ops, kvc, ca, dev, log):

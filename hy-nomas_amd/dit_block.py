@@ -82,8 +82,10 @@ class FP8DiTBlock(nn.Module):
         self.q_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
         self.k_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
 
-    def forward(self, img, vec, cos, sin, kv_cache, cache_valid_len: int,
-                update_cache: bool = False):
+    def pre_attention(self, img, vec, cos, sin):
+        """Image-stream half of nomas_compile_prepost.pre_attention (:29-72):
+        adaLN parts, LayerNorm + modulate, fused FP8 QKV, per-head RMSNorm, RoPE.
+        Returns q, k, v [B, L, H, D] bf16 and the six modulation parts."""
         B, L, C = img.shape
         H, D = self.heads, self.head_dim
         with stage("modulation"):
@@ -100,11 +102,13 @@ class FP8DiTBlock(nn.Module):
             q = (q.float() * c + _rotate_half(q) * s).type_as(v)
             k = (k.float() * c + _rotate_half(k) * s).type_as(v)
             v = v.contiguous()
-        if update_cache:
-            with stage("kv_write_fp8"):
-                quantize_kv_pair_into(kv_cache, k, v, cache_valid_len)
-        with stage("cache_attention"):
-            attn = chunk_attention(q, kv_cache, cache_valid_len, k_cur=k, v_cur=v)
+        return q, k, v, parts
+
+    def post_attention(self, img, attn, parts):
+        """Image-stream half of nomas_compile_prepost.post_attention (:75-99):
+        out-projection and gated residual, LayerNorm + modulate, FFN with
+        GELU-tanh fused into fc1's epilogue, gated residual."""
+        B, L, C = img.shape
         with stage("post_fp8"):
             img = img + fp8_linear(self.proj, attn.reshape(B, L, C)) * parts[2].unsqueeze(1)
             h = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[3], parts[4])
@@ -112,6 +116,16 @@ class FP8DiTBlock(nn.Module):
             h = fp8_linear(self.fc2, h)
             img = img + h * parts[5].unsqueeze(1)
         return img
+
+    def forward(self, img, vec, cos, sin, kv_cache, cache_valid_len: int,
+                update_cache: bool = False):
+        q, k, v, parts = self.pre_attention(img, vec, cos, sin)
+        if update_cache:
+            with stage("kv_write_fp8"):
+                quantize_kv_pair_into(kv_cache, k, v, cache_valid_len)
+        with stage("cache_attention"):
+            attn = chunk_attention(q, kv_cache, cache_valid_len, k_cur=k, v_cur=v)
+        return self.post_attention(img, attn, parts)
 
 
 class FP8ARModel(nn.Module):

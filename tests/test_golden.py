@@ -87,6 +87,8 @@ def test_gpu_kv_write_matches_golden(dev, fmt):
     B, Lt, H, D = x.shape
     make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
     cache = make(B, Lt + 3, H, D, device=dev)
+    for t in cache.values():                      # the cache is allocated uninitialised
+        t.view(torch.uint8).zero_()
     kvc.quantize_kv_pair_into(cache, x, x, 2)
     codes = u8(cache["k"][:, 2:2 + Lt])
     want_q = G["kv_q_fp8"] if fmt == "fp8" else G["kv_q_int8"].view(np.uint8)

@@ -1,0 +1,218 @@
+"""One FP8 DiT block (config 4 structure, reduced width) and the AR chunk loop
+(config 5 structure, reduced depth) on the GPU.
+
+The reference block (nomas_compile_prepost.py:14-99 with RMSNorm
+norm_layers.py:49-63 and RoPE posemb_layers.py:133-188,401-453) is restated on
+the CPU with the reference's own bf16 dtype flow: LayerNorm, modulation,
+RMSNorm, RoPE and residual adds run as the reference runs them on bf16
+tensors. Only its F.linear calls change: each becomes the FP8 linear's
+definition, per-token e4m3 activations (cutlass_fp8.py:35-41 with 1 x K
+blocks) times the same per-channel e4m3 weights, accumulated in fp32, plus
+bias (and GELU-tanh for fc1), rounded to bf16. Attention is fp32 softmax over
+the dequantized FP8 cache followed by the current chunk's bf16 K/V.
+
+Each stage (pre-attention, cached attention, post-attention) is checked on the
+GPU's own inputs to that stage, at the north-star tolerance. End to end, a
+1-ulp bf16 difference at a quantizer's input flips that element's e4m3 code
+by one step (up to 12.5 %), so differences grow from stage to stage; the
+end-to-end bound below is set from that effect and stated with it."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import assert_close_bf16, pkg_module
+
+pytestmark = pytest.mark.gpu
+
+# End to end, the block's update (out - img) versus the CPU restatement. The
+# update is about 1/10 of the residual stream here, so one bf16 ulp of the
+# residual is ~4 % of a typical update element; with code flips at the four
+# quantizers the measured update rel-L2 is 1.8e-2 (output 1.6e-3), while each
+# stage on identical inputs is within 2e-4 .. 4e-3.
+UPDATE_REL_L2 = 5e-2
+OUTPUT_REL_L2 = 1e-2
+
+
+def _fake_quant_rows(x):
+    """Per-row e4m3 round trip in fp32, the recipe of the activation quantizer."""
+    s = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-4) / 448.0
+    return (x / s).to(torch.float8_e4m3fn).float() * s
+
+
+def _ref_linear(m, x, gelu=False):
+    """FP8 linear on bf16 x: fp32 accumulate of e4m3 x e4m3 with scales, + bias, bf16 out."""
+    w = m.weight_q.float().cpu() * m.weight_scale.float().cpu().reshape(-1, 1)
+    y = _fake_quant_rows(x.float().reshape(-1, x.shape[-1])) @ w.T + m.bias.float().cpu()
+    if gelu:
+        y = F.gelu(y, approximate="tanh")
+    return y.to(torch.bfloat16).reshape(*x.shape[:-1], -1)
+
+
+def _modulate(x, shift, scale):
+    return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+def _rms_norm(x, weight, eps):
+    y = x.float()
+    y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + eps)
+    return y.to(x.dtype) * weight
+
+
+def _rotate_half(x):
+    real, imag = x.float().reshape(*x.shape[:-1], -1, 2).unbind(-1)
+    return torch.stack((-imag, real), dim=-1).flatten(3)
+
+
+def _cpu(t):
+    return t.detach().cpu()
+
+
+def ref_pre(blk, img, vec, cos, sin):
+    img, vec = _cpu(img), _cpu(vec)
+    B, L, C = img.shape
+    H, D = blk.heads, blk.head_dim
+    parts = F.linear(F.silu(vec), _cpu(blk.mod.weight), _cpu(blk.mod.bias)).chunk(6, dim=-1)
+    x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
+    q, k, v = _ref_linear(blk.qkv, x).view(B, L, 3, H, D).unbind(2)
+    q = _rms_norm(q, _cpu(blk.q_norm), 1e-6).to(v)
+    k = _rms_norm(k, _cpu(blk.k_norm), 1e-6).to(v)
+    c = _cpu(cos).view(1, L, 1, D)
+    s = _cpu(sin).view(1, L, 1, D)
+    q = (q.float() * c + _rotate_half(q) * s).type_as(v)
+    k = (k.float() * c + _rotate_half(k) * s).type_as(v)
+    return q, k, v, parts
+
+
+def ref_attention(q, k, v, hist_k, hist_v):
+    """fp32 softmax(q K^T / sqrt(D)) V over [dequantized history | current bf16 K/V]."""
+    q, k, v = _cpu(q).float(), _cpu(k).float(), _cpu(v).float()
+    keys = torch.cat([hist_k, k], dim=1)
+    vals = torch.cat([hist_v, v], dim=1)
+    out = torch.empty_like(q)
+    for h in range(q.shape[2]):
+        p = torch.softmax(q[0, :, h] @ keys[0, :, h].T / math.sqrt(q.shape[-1]), dim=-1)
+        out[0, :, h] = p @ vals[0, :, h]
+    return out
+
+
+def ref_post(blk, img, attn, parts):
+    img, attn = _cpu(img), _cpu(attn).to(torch.bfloat16)
+    parts = [_cpu(p) for p in parts]
+    B, L, C = img.shape
+    img = img + _ref_linear(blk.proj, attn.reshape(B, L, C)) * parts[2].unsqueeze(1)
+    h = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[3], parts[4])
+    h = _ref_linear(blk.fc2, _ref_linear(blk.fc1, h, gelu=True))
+    return img + h * parts[5].unsqueeze(1)
+
+
+def _rel(a, b):
+    a, b = _cpu(a).double(), _cpu(b).double()
+    return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+
+def _setup(dev):
+    db = pkg_module("dit_block")
+    kvc = pkg_module("fp8_kv_cache")
+    hidden, heads, (frames, hgt, wid) = 512, 4, (2, 6, 11)     # 132 tokens per chunk
+    L = frames * hgt * wid
+    g = torch.Generator(device=dev).manual_seed(7)
+    blk = db.FP8DiTBlock(hidden, heads, device=dev, generator=g)
+    cache = kvc.make_fp8_kv_block(1, 4 * L, heads, 128, device=dev)
+    for buf in cache.values():                    # allocated uninitialised, as in the reference
+        buf.view(torch.uint8).zero_()
+    hist = 2 * L + 37                             # ragged history length
+    hk, hv = _fill_history(dev, cache, hist, heads, 128, 11)
+    img = torch.randn(1, L, hidden, device=dev, generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, hidden, device=dev, generator=g).to(torch.bfloat16)
+    cos, sin = db.rope_tables(frames, hgt, wid, t_offset=5, device=dev)
+    return blk, cache, hist, hk, hv, img, vec, cos, sin, L
+
+
+def _fill_history(dev, cache, n, H, D, seed):
+    kvc = pkg_module("fp8_kv_cache")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k = (torch.randn(1, n, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn(1, n, H, D, device=dev, generator=g).to(torch.bfloat16)
+    kvc.quantize_kv_pair_into(cache, k, v, 0)
+    dq = lambda key: (cache[key][:, :n].float() * cache[key + "_scale"][:, :n]).cpu()
+    return dq("k"), dq("v")
+
+
+def test_block_stages_match_reference(dev):
+    print("case dit block stages", flush=True)
+    ca = pkg_module("cache_attention")
+    blk, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev)
+    with torch.no_grad():
+        q, k, v, parts = blk.pre_attention(img, vec, cos, sin)
+        rq, rk, rv, rparts = ref_pre(blk, img, vec, cos, sin)
+        for name, got, want in (("q", q, rq), ("k", k, rk), ("v", v, rv)):
+            print(f"pre {name} rel-L2 {_rel(got.float(), want.float()):.3e}", flush=True)
+            assert_close_bf16(_cpu(got).float().numpy(), want.float().numpy(), what=f"pre-attention {name}")
+        attn = ca.chunk_attention(q, cache, hist, k_cur=k, v_cur=v)
+        ra = ref_attention(q, k, v, hk, hv)
+        print(f"attention rel-L2 {_rel(attn.float(), ra):.3e}", flush=True)
+        assert_close_bf16(_cpu(attn).float().numpy(), ra.numpy(), what="cached attention")
+        out = blk.post_attention(img, attn, parts)
+        ro = ref_post(blk, img, attn, parts)
+        upd, rupd = _cpu(out).float() - _cpu(img).float(), ro.float() - _cpu(img).float()
+        print(f"post update rel-L2 {_rel(upd, rupd):.3e}", flush=True)
+        assert_close_bf16(_cpu(out).float().numpy(), ro.float().numpy(), what="post-attention")
+        assert _rel(upd, rupd) <= 2e-2
+
+
+@pytest.mark.parametrize("update_cache", [False, True])
+def test_block_end_to_end(dev, update_cache):
+    print(f"case dit block end to end update_cache={update_cache}", flush=True)
+    blk, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev)
+    with torch.no_grad():
+        out = blk(img, vec, cos, sin, cache, hist, update_cache=update_cache)
+        rq, rk, rv, rparts = ref_pre(blk, img, vec, cos, sin)
+        ro = ref_post(blk, img, ref_attention(rq, rk, rv, hk, hv), rparts)
+    got, want, x = _cpu(out).float(), ro.float(), _cpu(img).float()
+    rel_upd, rel_out = _rel(got - x, want - x), _rel(got, want)
+    print(f"block update rel-L2 {rel_upd:.3e}, output rel-L2 {rel_out:.3e}", flush=True)
+    assert torch.isfinite(got).all()
+    assert rel_out <= OUTPUT_REL_L2 and rel_upd <= UPDATE_REL_L2
+    written = cache["k"][:, hist:hist + L].view(torch.uint8)
+    assert bool(written.any()) == update_cache
+    assert not cache["k"][:, hist + L:].view(torch.uint8).any()
+    if update_cache:                               # the write is the KV kernel on this pass's K/V
+        _, k, v, _ = blk.pre_attention(img, vec, cos, sin)
+        kvc = pkg_module("fp8_kv_cache")
+        check = kvc.make_fp8_kv_block(1, L, blk.heads, 128, device=dev)
+        kvc.quantize_kv_pair_into(check, k, v, 0)
+        assert torch.equal(written, check["k"].view(torch.uint8))
+        assert torch.equal(cache["v"][:, hist:hist + L].view(torch.uint8), check["v"].view(torch.uint8))
+
+
+def test_ar_chunk_loop_structure(dev):
+    """Two chunks through a 2-block model: each chunk runs the denoising passes
+    without cache writes, then one write pass; the valid length advances by a
+    chunk; the second chunk attends to the first (its output differs from a
+    fresh model's on the same input); runs are deterministic."""
+    print("case ar chunk loop", flush=True)
+    db = pkg_module("dit_block")
+    kw = dict(depth=2, hidden=256, heads=2, latent_shape=(1, 4, 5), max_chunks=3, device=dev)
+    m1, m2 = db.FP8ARModel(seed=3, **kw), db.FP8ARModel(seed=3, **kw)
+    for c in m1.caches:                           # allocated uninitialised, as in the reference
+        c["k"].view(torch.uint8).zero_()
+    L = m1.tokens_per_chunk
+    g = torch.Generator(device=dev).manual_seed(9)
+    noise = [torch.randn(1, L, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(2)]
+    vecs = [torch.randn(1, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+    sig = torch.linspace(1.0, 0.0, 4).tolist()
+    x0 = m1.generate_chunk(noise[0], vecs[:3], vecs[3], sig)
+    assert m1.cache_valid_len == L and m1.frames_done == 1
+    for c in m1.caches:
+        assert c["k"][:, :L].view(torch.uint8).any() and not c["k"][:, L:].view(torch.uint8).any()
+    x1 = m1.generate_chunk(noise[1], vecs[:3], vecs[3], sig)
+    assert m1.cache_valid_len == 2 * L
+    y0 = m2.generate_chunk(noise[0], vecs[:3], vecs[3], sig)
+    assert torch.equal(x0, y0)                                  # deterministic
+    m3 = db.FP8ARModel(seed=3, **kw)
+    m3.frames_done = 1                                         # same RoPE offset, empty cache
+    z1 = m3.generate_chunk(noise[1], vecs[:3], vecs[3], sig)
+    assert not torch.equal(x1, z1)                              # history changes the result
+    assert torch.isfinite(x1).all()
