@@ -564,7 +564,9 @@ static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t
     const int64_t target = 2LL * cus;
     if (work <= 0 || work >= target) return 1;
     const int64_t tiles = (kv_len + cur_len + attn::BKV - 1) / attn::BKV;
-    int64_t sp = (target + work - 1) / work;
+    // Round down: the kernel holds two workgroups per CU, so work * sp <= target
+    // keeps the whole launch in one round (one more workgroup would need a second).
+    int64_t sp = target / work;
     const int64_t cap = tiles / 16;
     if (sp > cap) sp = cap;
     return sp > 1 ? (int)sp : 1;

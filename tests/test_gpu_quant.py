@@ -47,6 +47,54 @@ def test_rows_fp8_special_values(O, dev):
         assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
+def _edge_rows(cols):
+    """Rows around the quantizers' quotient paths: signed zeros and bf16
+    subnormals under a normal row maximum; row maxima just above and just below
+    the point (s = 2^-100) where the kernels switch to the IEEE division;
+    negative zero rows; and extreme-range rows (1e38 next to tiny values)."""
+    rng = np.random.default_rng(17)
+    rows = []
+    r = (rng.integers(0, 0x3F80, cols) | (rng.integers(0, 2, cols) << 15)).astype(np.uint16)
+    r[:8] = [0x3F80, 0x8000, 0x0000, 0x8001, 0x0001, 0x807F, 0x0080, 0xBF80]
+    rows.append(r)
+    for top in (0x1200, 0x1210, 0x11F0, 0x1180, 0x0F00):   # 2^-91 (s ~ 2^-99.8) .. 2^-97
+        r = (rng.integers(0, top + 1, cols) | (rng.integers(0, 2, cols) << 15)).astype(np.uint16)
+        r[0] = top
+        rows.append(r)
+    rows.append(np.full(cols, 0x8000, np.uint16))            # all -0.0
+    r = (rng.integers(0, 0x7F7F, cols) | (rng.integers(0, 2, cols) << 15)).astype(np.uint16)
+    r[0] = 0x7F7F                                             # bf16 max with every magnitude below it
+    rows.append(r)
+    return np.stack(rows)
+
+
+def test_rows_fp8_quotient_edge_rows(O, dev):
+    print("case rows_fp8 quotient edge rows", flush=True)
+    ops = pkg_module("ops")
+    bits = _edge_rows(1024)
+    x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    for mode in (0, 1):
+        q, s = ops.quantize_rows_fp8(x.to(dev), mode, 1e-4)
+        qo, so = O.quantize_rows_fp8(bits, mode)
+        assert np.array_equal(u8(q), qo), f"mode {mode} codes"
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_kv_quantize_quotient_edge_rows(O, dev, fmt):
+    print(f"case kv quotient edge rows {fmt}", flush=True)
+    kvc = pkg_module("fp8_kv_cache")
+    bits = _edge_rows(128)                                    # one (token, head) row each
+    n = bits.shape[0]
+    x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).reshape(1, n, 1, 128)
+    make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
+    cache = make(1, n, 1, 128, device=dev)
+    kvc.quantize_kv_pair_into(cache, x.to(dev), x.to(dev), 0)
+    qo, so = O.kv_quantize(bits.reshape(1, n, 1, 128), O.KV_FP8 if fmt == "fp8" else O.KV_INT8)
+    assert np.array_equal(u8(cache["k"]), qo) and np.array_equal(u8(cache["v"]), qo)
+    assert np.array_equal(cache["k_scale"].cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
 def test_rows_fp8_strided_input(O, dev):
     ops = pkg_module("ops")
     x = _gen((64, 512), 11)
