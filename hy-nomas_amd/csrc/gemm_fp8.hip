@@ -23,6 +23,8 @@
 // The MFMA's first operand is the weight tile and its second the activation
 // tile, i.e. the wave computes out^T: each lane then holds four consecutive
 // output columns n..n+3 of one row m and stores them as one 8-byte write.
+#include <type_traits>
+
 #include "hn_capi_internal.h"
 #include "hn_common.h"
 
@@ -53,7 +55,12 @@ struct Params {
     int64_t M, N, K, ldc;
     int act;
     int tiles_m, tiles_n;
-    int per_xcd;  // ceil(tiles / 8)
+    int per_xcd;  // work items per XCD (grid = 8 * per_xcd)
+    // Row/column kernel order: the tiles_full = tm_full * tn_full tiles that
+    // lie wholly inside M x N come first, then the tiles_part edge tiles
+    // (the last row stripe if M % 256 != 0, then the last column stripe if
+    // N % 256 != 0); each class is split evenly over the 8 XCDs.
+    int tm_full, tn_full, tiles_full, tiles_part, m_tail;
 };
 
 // 16-byte chunk c of LDS row r lives at chunk position c ^ ((r >> 1) & 7).
@@ -152,21 +159,85 @@ HN_DEVICE void interleave_reads_with_mfma() {
 }
 
 HN_DEVICE float gelu_tanh(float x) {
-    // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), with
-    // tanh(u) = 1 - 2 / (2^{2u log2 e} + 1) on v_exp_f32 / v_rcp_f32 (about
-    // 1 ulp each: far below the bf16 output's rounding). Saturates correctly:
-    // u -> +inf gives 1, u -> -inf gives -1.
-    const float u2 = x * fmaf(0.044715f * 2.0f * 0.7978845608028654f * 1.4426950408889634f, x * x,
-                              2.0f * 0.7978845608028654f * 1.4426950408889634f);
-    const float e = __builtin_amdgcn_exp2f(u2);
-    const float t = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
-    return 0.5f * x * (1.0f + t);
+    // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), written as
+    // x * sigmoid(2u) = x / (1 + 2^t), t = -2 u log2(e) = x (c0 + c1 x^2), on
+    // v_exp_f32 / v_rcp_f32 (about 1 ulp each: far below the bf16 output's
+    // rounding). Saturates correctly: x -> -inf gives 2^t = inf and -0;
+    // x -> +inf gives 2^t = 0 and x.
+    constexpr float c0 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+    constexpr float c1 = c0 * 0.044715f;
+    const float t = x * fmaf(c1, x * x, c0);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 HN_DEVICE uint32_t pack_bf16(float a, float b) {
     const f32x2_t f = {a, b};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// Epilogue shared by the kernels. acc[i][j][v] holds out^T for n = wn*128 +
+// 32 i + 8 (v/4) + 4 (lane/32) + v%4 and m = wm*128 + 32 j + lane%32
+// (tile-local). Each wave scales its 128 x 128 sub-tile, packs it to bf16 and
+// parks it in its own LDS slice; then it writes the slice out as 256-byte row
+// segments (16 lanes x 16 bytes per row, 4 rows per store).
+template <int MODE>
+HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_t n0, uint8_t* smem,
+                        int wave, int wm, int wn, int lane, int imax = 4, int jmax = 4) {
+    __syncthreads();  // the last K step's LDS reads are done (all waves)
+    uint8_t* ow = smem + wave * OUT_WAVE_BYTES;
+    float sam[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+        m = m < p.M ? m : p.M - 1;
+        sam[j] = MODE == ROWCOL ? p.sa[m] : 1.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (i >= imax) continue;  // weight block wholly past N (wave-uniform)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+            int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
+            n = n < p.N ? n : p.N - 4;  // stays in bounds; columns past N are not stored
+            float sbn[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (MODE == ROWCOL) {
+                const float4 s4 = *reinterpret_cast<const float4*>(p.sb + n);
+                sbn[0] = s4.x; sbn[1] = s4.y; sbn[2] = s4.z; sbn[3] = s4.w;
+                if (p.bias) {
+                    const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+                    bn[0] = bf16_bits_to_f32(bb.x & 0xffffu); bn[1] = bf16_bits_to_f32(bb.x >> 16);
+                    bn[2] = bf16_bits_to_f32(bb.y & 0xffffu); bn[3] = bf16_bits_to_f32(bb.y >> 16);
+                }
+            }
+            const int nl = i * 32 + vq * 8 + (lane >> 5) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j >= jmax) continue;  // activation block wholly past M (wave-uniform)
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = fmaf(acc[i][j][vq * 4 + e], sam[j] * sbn[e], bn[e]);
+                    if (MODE == ROWCOL && p.act == HN_ACT_GELU_TANH) y[e] = gelu_tanh(y[e]);
+                }
+                const int ml = j * 32 + (lane & 31);
+                *reinterpret_cast<uint2*>(ow + ml * OUT_ROW + nl * 2) =
+                    make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+            }
+        }
+    }
+    // Each wave reads back only its own slice: no barrier needed beyond the
+    // wave's own LDS ordering.
+    __builtin_amdgcn_s_waitcnt(0);
+    const int64_t nbase = n0 + wn * 128 + (lane & 15) * 8;
+#pragma unroll 4
+    for (int r = 0; r < 32; ++r) {
+        const int ml = r * 4 + (lane >> 4);
+        const int64_t m = m0 + wm * 128 + ml;
+        const uint4 v = *reinterpret_cast<const uint4*>(ow + ml * OUT_ROW + (lane & 15) * 16);
+        if (m < p.M && nbase < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + nbase) = v;
+    }
+
 }
 
 template <int MODE>
@@ -315,61 +386,228 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
     }
     }
 
-    // Epilogue. acc[i][j][v] holds out^T for n = wn*128 + 32 i + 8 (v/4) +
-    // 4 (lane/32) + v%4 and m = wm*128 + 32 j + lane%32 (tile-local). Each
-    // wave scales its 128 x 128 sub-tile, packs it to bf16 and parks it in its
-    // own LDS slice; then it writes the slice out as 256-byte row segments
-    // (16 lanes x 16 bytes per row, 4 rows per store).
-    __syncthreads();  // the last K step's LDS reads are done (all waves)
-    uint8_t* ow = smem + wave * OUT_WAVE_BYTES;
-    float sam[4];
+    epilogue<MODE>(acc, p, m0, n0, smem, wave, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Row/column-scaled kernel with a five-stage pipeline.
+//
+// One wave per SIMD holds the 128 x 128 accumulator, so nothing else on the
+// SIMD hides memory latency: the K loop itself must. Stages here are 64 bytes
+// of K (A and B, 16 KB each = 32 KB), and five of them fill the 160 KB of LDS.
+// Stage s is requested four K steps before it is consumed, so each DMA has
+// three full K steps (about 3 x 1000 MFMA cycles) to arrive -- L2 misses that
+// go to the Infinity Cache or HBM included. The 16 MFMAs of a K step are
+// split in two halves around the per-step wait + barrier: the first half
+// runs on fragments already in registers while the wave waits, the second
+// half covers the LDS reads of the next step's fragments.
+constexpr int P_BK = 64;
+constexpr int P_STAGES = 5;
+constexpr int P_TILE = BM * P_BK;            // one operand, 16 KB
+constexpr int P_STAGE = 2 * P_TILE;          // A + B, 32 KB
+constexpr int P_SMEM = P_STAGES * P_STAGE;   // 160 KB
+static_assert(P_SMEM >= 4 * OUT_WAVE_BYTES, "epilogue staging must fit in the stage buffers");
+constexpr int P_DMA_PER_STAGE = 8;           // global_load_lds per wave per stage (4 A + 4 B)
+
+// 16-byte chunk c (0..3) of 64-byte LDS row r sits at position c ^ ((r >> 2) & 3):
+// 16 consecutive rows then cover all 16 bank groups of a 256-byte LDS cycle
+// (row r starts at bank group 4 (r & 3)).
+HN_DEVICE int pswz(int row, int chunk) { return row * P_BK + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+// Stage loads use global_load_lds with a scalar base: the address is
+// sbase (SGPR pair: operand + tile row0 * K + k0) + voff (per-lane 32-bit
+// offset of the lane's row and chunk inside the tile, fixed for the tile), and
+// the LDS destination M0 is scalar too. Issuing a 1 KB load is then one s_mov
+// and the load -- no per-load vector address arithmetic or readfirstlane, so
+// the eight loads of a K step cost a few dozen issue cycles.
+HN_DEVICE void dma_16B_sbase(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory", "m0");
+}
+
+// Per-lane offsets of a wave's four 1 KB regions (16 rows of 64 bytes) of one
+// 256 x 64 stage operand. Lane l lands at row l / 4, position l % 4 of region
+// wave * 4 + q and fetches the logical chunk that position holds. Rows past
+// the operand's end are clamped to its last row: in bounds, never stored.
+HN_DEVICE void stage_offsets(uint32_t (&off)[4], int64_t row0, int64_t rows, int64_t K, int wave,
+                             int lane) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-        m = m < p.M ? m : p.M - 1;
-        sam[j] = MODE == ROWCOL ? p.sa[m] : 1.0f;
+    for (int q = 0; q < 4; ++q) {
+        const int r = (wave * 4 + q) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+        off[q] = (uint32_t)((row - row0) * K + (c << 4));
     }
+}
+
+HN_DEVICE i32x8 pread_frag(const uint8_t* lds, int row, int lane) {
+    const int c0 = (lane >> 5) * 2;
+    const uint4 lo = *reinterpret_cast<const uint4*>(lds + pswz(row, c0));
+    const uint4 hi = *reinterpret_cast<const uint4*>(lds + pswz(row, c0 + 1));
+    i32x8 f;
+    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+    return f;
+}
+
+HN_DEVICE void read_pfrags(Frags& f, const uint8_t* st, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.b[i] = pread_frag(st + P_TILE, wn * 128 + i * 32 + (lane & 31), lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.a[j] = pread_frag(st, wm * 128 + j * 32 + (lane & 31), lane);
+}
+
+// MFMAs of weight blocks i in [I0, I0 + 2) against all four activation blocks.
+template <int I0>
+HN_DEVICE void mfma_half(f32x16 (&acc)[4][4], const Frags& f) {
+#pragma unroll
+    for (int i = I0; i < I0 + 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
+}
+
+// mfma_half for an edge tile: only blocks inside the matrix (wave-uniform tests).
+template <int I0>
+HN_DEVICE void mfma_half_partial(f32x16 (&acc)[4][4], const Frags& f, int imax, int jmax) {
+#pragma unroll
+    for (int i = I0; i < I0 + 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (i < imax && j < jmax) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
+}
+
+// Wait until at most `stages` of this wave's stage loads are still in flight.
+HN_DEVICE void wait_stages_in_flight(int stages) {
+    switch (stages) {
+        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+static_assert(P_DMA_PER_STAGE == 8, "wait_stages_in_flight counts 8 loads per stage");
+
+// Work item (XCD x = id % 8, position i = id / 8 in that XCD's queue) -> tile.
+// An XCD's queue holds its share of the full tiles, in groups of GROUP_M tile
+// rows walking N (so the ~32 tiles it runs at once share A and B panels in its
+// L2), followed by its share of the edge tiles. Edge tiles skip the MFMAs of
+// blocks outside the matrix and so run shorter; queued last, they fill the
+// final round instead of adding one: at the north-star shape (43 x 48 tiles,
+// the last tile row 48 rows deep) each XCD gets 252 full and 6 half-length
+// tiles -- eight rounds of its 32 CUs instead of nine.
+HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) {
+    const int x = id & 7, i = id >> 3;
+    const int F = p.tiles_full, P = p.tiles_part;
+    const int fx = F / 8 + (x < F % 8 ? 1 : 0);
+    if (i < fx) {
+        const int f = x * (F / 8) + min(x, F % 8) + i;
+        const int per_group = GROUP_M * p.tn_full;
+        const int first_m = (f / per_group) * GROUP_M;
+        const int gm = min(GROUP_M, p.tm_full - first_m);
+        tm = first_m + (f % per_group) % gm;
+        tn = (f % per_group) / gm;
+        return true;
+    }
+    const int q = i - fx;
+    if (q >= P / 8 + (x < P % 8 ? 1 : 0)) return false;
+    int g = x * (P / 8) + min(x, P % 8) + q;
+    if (p.m_tail) {
+        if (g < p.tiles_n) { tm = p.tm_full; tn = g; return true; }
+        g -= p.tiles_n;
+    }
+    tm = g;
+    tn = p.tn_full;
+    return true;
+}
+
+__global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[P_SMEM];
+    int tm, tn;
+    if (!tile_of(p, blockIdx.x, tm, tn)) return;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int KT = (int)(p.K / P_BK);
+    const uint8_t* const a_tile = p.a + m0 * p.K;
+    const uint8_t* const b_tile = p.b + n0 * p.K;
+    uint32_t off_a[4], off_b[4];
+    stage_offsets(off_a, m0, p.M, p.K, wave, lane);
+    stage_offsets(off_b, n0, p.N, p.K, wave, lane);
+    const uint32_t lds_base = lds_addr(smem) + wave * 4 * 1024;
+    // Blocks of this wave inside the matrix: imax weight blocks (N % 128 == 0,
+    // so 0 or 4), jmax activation blocks of 32 rows. Wave-uniform.
+    const int64_t rows_w = p.M - (m0 + wm * 128), cols_w = p.N - (n0 + wn * 128);
+    const int jmax = rows_w >= 128 ? 4 : (rows_w <= 0 ? 0 : (int)((rows_w + 31) >> 5));
+    const int imax = cols_w >= 128 ? 4 : (cols_w <= 0 ? 0 : (int)(cols_w >> 5));
+    const bool whole = imax == 4 && jmax == 4;
+
+    f32x16 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-            int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
-            n = n < p.N ? n : p.N - 4;  // stays in bounds; columns past N are not stored
-            float sbn[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (MODE == ROWCOL) {
-                const float4 s4 = *reinterpret_cast<const float4*>(p.sb + n);
-                sbn[0] = s4.x; sbn[1] = s4.y; sbn[2] = s4.z; sbn[3] = s4.w;
-                if (p.bias) {
-                    const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
-                    bn[0] = bf16_bits_to_f32(bb.x & 0xffffu); bn[1] = bf16_bits_to_f32(bb.x >> 16);
-                    bn[2] = bf16_bits_to_f32(bb.y & 0xffffu); bn[3] = bf16_bits_to_f32(bb.y >> 16);
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    auto issue = [&](int s) {
+        const uint32_t st = lds_base + (s % P_STAGES) * P_STAGE;
+        const int64_t k0 = (int64_t)s * P_BK;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dma_16B_sbase(a_tile + k0, off_a[q], st + q * 1024);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dma_16B_sbase(b_tile + k0, off_b[q], st + P_TILE + q * 1024);
+    };
+    const int pre = KT < P_STAGES - 1 ? KT : P_STAGES - 1;
+    for (int s = 0; s < pre; ++s) issue(s);
+    wait_stages_in_flight(pre - 1);
+    __syncthreads();
+
+    // The K loop, instantiated for whole tiles and for edge tiles (blocks
+    // outside the matrix skipped); the choice is made once per tile.
+    auto kloop = [&](auto edge_tag) {
+        constexpr bool EDGE = decltype(edge_tag)::value;
+        // One K step on fragments `cur`, prefetching the next step into `nxt`.
+        auto step = [&](int kt, Frags& cur, Frags& nxt) {
+            // Stage kt+4 reuses the buffer of stage kt-1, which every wave
+            // finished reading before the previous step's barrier.
+            if (kt + P_STAGES - 1 < KT) issue(kt + P_STAGES - 1);
+            if (EDGE) mfma_half_partial<0>(acc, cur, imax, jmax);
+            else mfma_half<0>(acc, cur);
+            if (kt + 1 < KT) {
+                const int last = kt + P_STAGES - 1 < KT ? kt + P_STAGES - 1 : KT - 1;
+                wait_stages_in_flight(last - (kt + 1));  // stage kt+1 landed (this wave's part)
+                __syncthreads();                          // ... and every wave's part
+                read_pfrags(nxt, smem + ((kt + 1) % P_STAGES) * P_STAGE, wm, wn, lane);
+            }
+            if (EDGE) {
+                mfma_half_partial<2>(acc, cur, imax, jmax);
+            } else {
+                mfma_half<2>(acc, cur);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two DS reads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
                 }
             }
-            const int nl = i * 32 + vq * 8 + (lane >> 5) * 4;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float y[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    y[e] = fmaf(acc[i][j][vq * 4 + e], sam[j] * sbn[e], bn[e]);
-                    if (MODE == ROWCOL && p.act == HN_ACT_GELU_TANH) y[e] = gelu_tanh(y[e]);
-                }
-                const int ml = j * 32 + (lane & 31);
-                *reinterpret_cast<uint2*>(ow + ml * OUT_ROW + nl * 2) =
-                    make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
-            }
+        };
+        Frags f0, f1;
+        read_pfrags(f0, smem, wm, wn, lane);
+        int kt = 0;
+        for (; kt + 1 < KT; kt += 2) {
+            step(kt, f0, f1);
+            step(kt + 1, f1, f0);
         }
-    // Each wave reads back only its own slice: no barrier needed beyond the
-    // wave's own LDS ordering.
-    __builtin_amdgcn_s_waitcnt(0);
-    const int64_t nbase = n0 + wn * 128 + (lane & 15) * 8;
-#pragma unroll 4
-    for (int r = 0; r < 32; ++r) {
-        const int ml = r * 4 + (lane >> 4);
-        const int64_t m = m0 + wm * 128 + ml;
-        const uint4 v = *reinterpret_cast<const uint4*>(ow + ml * OUT_ROW + (lane & 15) * 16);
-        if (m < p.M && nbase < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + nbase) = v;
-    }
+        if (kt < KT) step(kt, f0, f1);
+    };
+    if (whole) kloop(std::false_type{});
+    else kloop(std::true_type{});
+    epilogue<ROWCOL>(acc, p, m0, n0, smem, wave, wm, wn, lane, imax, jmax);
 }
 
 }  // namespace gemm
@@ -400,9 +638,15 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     HN_REQUIRE(tm * tn <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
     p.tiles_m = (int)tm; p.tiles_n = (int)tn;
     p.per_xcd = (int)((tm * tn + 7) / 8);
+    p.tm_full = (int)(M / gemm::BM);
+    p.tn_full = (int)(N / gemm::BN);
+    p.m_tail = (int)(M % gemm::BM != 0);
+    p.tiles_full = p.tm_full * p.tn_full;
+    p.tiles_part = (int)(tm * tn) - p.tiles_full;
+    if (mode == gemm::ROWCOL) p.per_xcd = (p.tiles_full + 7) / 8 + (p.tiles_part + 7) / 8;
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
     if (mode == gemm::ROWCOL)
-        gemm::gemm_fp8_kernel<gemm::ROWCOL><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+        gemm::gemm_rowcol_kernel<<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     else
         gemm::gemm_fp8_kernel<gemm::BLOCKWISE><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     return check_launch(who);

@@ -42,7 +42,8 @@ def _check_linear(O, dev, M, K, N, gelu, bias=True, rows=None):
     return assert_close_bf16(got, ref, what=f"linear {M}x{K}x{N} gelu={gelu}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 128, 128), (129, 256, 384), (300, 384, 256), (64, 12288, 3072)])
+@pytest.mark.parametrize("M,K,N", [(1, 128, 128), (129, 256, 384), (300, 384, 256), (64, 12288, 3072),
+                                   (1000, 256, 640), (2777, 384, 1152)])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_linear_fp8_small_shapes(O, dev, M, K, N, gelu):
     print(f"case linear {M}x{K}x{N} gelu={gelu}", flush=True)
