@@ -20,8 +20,9 @@
 // MFMA output puts one query per lane column, so the online-softmax max/sum
 // are lane-local plus one exchange with lane ^ 32. P^T is packed to fp16 in
 // registers and reused as the B operand of O^T += V^T P^T on
-// v_mfma_f32_32x32x16_f16 (V^T is transposed into LDS with a key order that
-// matches the S^T register layout). Two LDS
+// v_mfma_f32_32x32x16_f16. V is stored in LDS in its natural [key][dim] order
+// and the V^T operand is fetched with gfx950's transposing LDS read
+// (ds_read_b64_tr_b16), in the key order of the S^T registers. Two LDS
 // stages: the next tile's global loads are in flight in registers while the
 // MFMAs consume the current one.
 //
@@ -42,13 +43,12 @@ constexpr int NT = 64 * NW;
 constexpr int QW = 32;             // queries per wave
 constexpr int BQ = QW * NW;        // queries per workgroup
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
-// V^T tile row: 64 fp16 + 8 B pad. 136 B = 34 dwords: rows 16 apart start
-// 32 banks apart (each V^T store instruction writes such a row pair, 2 x 128 B,
-// so it covers all 64 banks once), and 32 consecutive rows start on 32
-// distinct even banks (conflict-free 8-byte fragment reads).
-constexpr int VROW = BKV * 2 + 8;
+// V tile: [key][dim] fp16 rows of 256 B, padded to 320 B (80 dwords: row k
+// starts 16 banks after row k - 1); 16-byte chunk c of key row k is stored at
+// position vchunk(k, c) (see below).
+constexpr int VROW = D * 2 + 64;
 constexpr int K_BYTES = BKV * KROW;
-constexpr int V_BYTES = D * VROW;
+constexpr int V_BYTES = BKV * VROW;
 constexpr int S_BYTES = 2 * BKV * 4;  // per-key K and V scales (fp32)
 constexpr int STAGE = K_BYTES + V_BYTES + S_BYTES;
 
@@ -77,12 +77,46 @@ struct Params {
     float* ws_ml;      // splits > 1: running max and sum, [split][B][H][Lq][2]
 };
 
-// Position of key j (0..63) of a tile inside a V^T row: within each 16-key
-// slice, bits 2 and 3 of the index are swapped. Slice t of the tile is then
-// laid out so that lane half h's eight k-slots of the PV MFMA are keys
-// {16t + 4h + 0..3, 16t + 8 + 4h + 0..3}, exactly the keys that lane holds
-// in S^T registers 8t' .. 8t'+7 (see compute_tile).
-HN_DEVICE int vpos(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Position of the 16-byte chunk c (8 dims) of key row k in the V tile: the two
+// low bits of c are XORed with bits 2-3 of k. With the 16-bank row shift this
+// makes both access patterns conflict-free over the 64 LDS banks: the row
+// writes (16 lanes = keys 16 i .. 16 i + 15 at one chunk index: bank groups
+// 16 (k % 4) + 4 ((c % 4) ^ (k / 4 % 4)) all differ) and the transposing reads
+// (keys 4 i .. 4 i + 3 x chunks 4 b .. 4 b + 3). Chunk groups 4 b .. 4 b + 3
+// stay in place, so a dim block is a constant offset.
+HN_DEVICE int vchunk(int k, int c) { return (c & ~3) | ((c & 3) ^ ((k >> 2) & 3)); }
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// V^T fragment of the PV MFMA for dim block db and 16-key slice `slice`:
+// lane l needs dim 32 db + l % 32 and keys 16 slice + 4 (l / 32) + {0..3} and
+// + 8 + {0..3} (the order of the P^T registers, see compute loop). The
+// transposing read gives lane i of each 16-lane group element i % 4 of the
+// 8-byte rows addressed by lanes i / 4 + 4 e, e = 0..3; so lane j of group g
+// addresses key (base + j / 4) at dims 32 db + 16 (g % 2) + 4 (j % 4), and
+// every lane receives four consecutive keys of its own dim.
+HN_DEVICE f16x8 read_vt(const uint8_t* vl, int db, int slice, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int c = 4 * db + 2 * (g & 1) + ((j & 3) >> 1);
+    const int byte = 8 * (j & 1);
+    f16x4 r[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+        const int k = 16 * slice + 8 * h2 + 4 * (g >> 1) + (j >> 2);
+        const uint8_t* a = vl + k * VROW + vchunk(k, c) * 16 + byte;
+        r[h2] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(__attribute__((address_space(3))) void*)a));
+    }
+    f16x8 v;
+    v[0] = r[0][0]; v[1] = r[0][1]; v[2] = r[0][2]; v[3] = r[0][3];
+    v[4] = r[1][0]; v[5] = r[1][1]; v[6] = r[1][2]; v[7] = r[1][3];
+    return v;
+}
 
 // Two codes (bytes 2 hi, 2 hi + 1 of w) -> their two exact bf16 values. The
 // gfx950 conversion is used with a unit scale only: its scale operand applies
@@ -112,9 +146,6 @@ HN_DEVICE void cvt16(const uint4& c, uint32_t (&o)[8]) {
     }
 }
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 HN_DEVICE uint32_t pack_f16(float a, float b) {
     const f32x2 f = {a, b};
@@ -145,12 +176,11 @@ HN_DEVICE uint32_t bf16x2_to_f16x2(uint32_t w) {
 // Registers holding one cache tile between its global load and its LDS
 // write (the load is issued before the tile in LDS is consumed).
 // K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
-// V: lane l of wave w owns keys 2 (l % 32), +1 and the 16 dims of group
-//    2 w + l / 32, so one store instruction of a wave writes two whole V^T rows.
+// V: lane l of wave w owns key l, dims 32 w .. 32 w + 31.
 struct CacheRegs {
     uint4 k[2];
     uint4 v[2];
-    float sk[2], sv[2];
+    float sk[2], sv;
 };
 
 HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t h,
@@ -165,30 +195,23 @@ HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t
         r.k[i] = *reinterpret_cast<const uint4*>(p.kc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (u & 7) * 16);
         r.sk[i] = p.ks[b * p.ss0 + tok * p.ss1 + h * p.ss2];
     }
-    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int64_t j = kp * 2 + i;
-        j = j < count ? j : count - 1;
-        const int64_t tok = first + j;
-        r.v[i] = *reinterpret_cast<const uint4*>(p.vc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + dg * 16);
-        r.sv[i] = p.vs[b * p.ss0 + tok * p.ss1 + h * p.ss2];
-    }
+    int64_t j = t & 63;
+    j = j < count ? j : count - 1;
+    const int64_t tok = first + j;
+    const uint8_t* src = p.vc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (t >> 6) * 32;
+    r.v[0] = *reinterpret_cast<const uint4*>(src);
+    r.v[1] = *reinterpret_cast<const uint4*>(src + 16);
+    r.sv = p.vs[b * p.ss0 + tok * p.ss1 + h * p.ss2];
 }
 
-// V^T write of 2 consecutive keys x 16 dims: cv[key][e] holds dims (2e, 2e+1).
-HN_DEVICE void store_vt(uint8_t* vl, const uint32_t (&cv)[2][8]) {
+// V row write: key t % 64, chunks 4 (t / 64) .. +3 (32 dims), from 16 dwords of fp16 pairs.
+HN_DEVICE void store_v_row(uint8_t* vl, const uint32_t (&cv)[16]) {
     const int t = threadIdx.x;
-    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
-    const int pos = vpos(kp * 2);  // the pair stays adjacent: vpos keeps bits 0-1
+    const int k = t & 63, c0 = 4 * (t >> 6);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = __builtin_amdgcn_perm(cv[1][e], cv[0][e], 0x05040100u);  // dim 2e
-        const uint32_t hi = __builtin_amdgcn_perm(cv[1][e], cv[0][e], 0x07060302u);  // dim 2e+1
-        const int d0 = dg * 16 + 2 * e;
-        *reinterpret_cast<uint32_t*>(vl + d0 * VROW + pos * 2) = lo;
-        *reinterpret_cast<uint32_t*>(vl + (d0 + 1) * VROW + pos * 2) = hi;
-    }
+    for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<uint4*>(vl + k * VROW + vchunk(k, c0 + c) * 16) =
+            make_uint4(cv[4 * c], cv[4 * c + 1], cv[4 * c + 2], cv[4 * c + 3]);
 }
 
 // Per-key scales in LDS: [0, 64) K scale * softmax_scale * log2 e, [64, 128) V scale.
@@ -208,14 +231,11 @@ HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st
         dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
         if ((u & 7) == 0) sc[u >> 3] = r.sk[i] * p.scale_log2;
     }
-    uint32_t cv[2][8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) codes16_f16<FMT>(r.v[i], cv[i]);
-    store_vt(st + K_BYTES, cv);
-    if (t < 32) {  // dim group 0: lane t holds keys 2 t, 2 t + 1
-        sc[BKV + t * 2] = r.sv[0];
-        sc[BKV + t * 2 + 1] = r.sv[1];
-    }
+    uint32_t cv[16];
+    codes16_f16<FMT>(r.v[0], *reinterpret_cast<uint32_t(*)[8]>(&cv[0]));
+    codes16_f16<FMT>(r.v[1], *reinterpret_cast<uint32_t(*)[8]>(&cv[8]));
+    store_v_row(st + K_BYTES, cv);
+    if (t < BKV) sc[BKV + t] = r.sv;  // wave 0: lane t holds key t
 }
 
 // Unquantized tail tile (bf16 K/V of the current chunk): load and write to LDS
@@ -235,20 +255,21 @@ HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t fir
         dst[0] = lo;
         dst[1] = hi;
     }
-    const int kp = t & 31, dg = ((t >> 6) << 1) | ((t >> 5) & 1);
-    uint32_t cv[2][8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int64_t j = kp * 2 + i;
+    {
+        int64_t j = t & 63;
         j = j < count ? j : count - 1;
-        const uint16_t* src = p.vcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + dg * 16;
-        const uint4 lo = *reinterpret_cast<const uint4*>(src);
-        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
-        const uint32_t b[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const uint16_t* src = p.vcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (t >> 6) * 32;
+        uint32_t cv[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) cv[i][e] = bf16x2_to_f16x2(b[e]);
+        for (int c = 0; c < 4; ++c) {
+            const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * c);
+            cv[4 * c] = bf16x2_to_f16x2(w.x);
+            cv[4 * c + 1] = bf16x2_to_f16x2(w.y);
+            cv[4 * c + 2] = bf16x2_to_f16x2(w.z);
+            cv[4 * c + 3] = bf16x2_to_f16x2(w.w);
+        }
+        store_v_row(st + K_BYTES, cv);
     }
-    store_vt(st + K_BYTES, cv);
     float* sc = stage_scales(st);
     if (t < BKV) sc[t] = p.scale_log2;
     else if (t < 2 * BKV) sc[t] = 1.0f;
@@ -469,10 +490,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
                 const int slice = kb * 2 + tt;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
-                    const uint8_t* vp = vl + (db * 32 + col) * VROW + (16 * slice + 8 * half) * 2;
-                    const uint2 v0 = *reinterpret_cast<const uint2*>(vp);
-                    const uint2 v1 = *reinterpret_cast<const uint2*>(vp + 8);
-                    const f16x8 vf = __builtin_bit_cast(f16x8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+                    const f16x8 vf = read_vt(vl, db, slice, lane);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kb][tt], o[db], 0, 0, 0);
                 }
             }
