@@ -118,7 +118,20 @@ def main():
 
     ms_linear = time_loop(lambda: ops.linear_fp8(x, qw, sw, bias, 1), args.steps, args.warmup)
     ms_gemm = time_loop(lambda: ops.gemm_fp8_rowcol(qx, qw, sx, sw, bias, 1), args.steps, args.warmup)
-    ms_quant = time_loop(lambda: ops.quantize_rows_fp8(x), args.steps, args.warmup)
+    # The short kernels are timed through the C ABI with preallocated outputs:
+    # at ~20 us per call, Python op dispatch would otherwise leave the GPU idle
+    # between launches and the loop would time the host.
+    L = importlib.import_module("hy-nomas_amd._lib")
+    lib = L.load()
+    qx_buf = torch.empty_like(qx)
+    sx_buf = torch.empty_like(sx)
+    stream_ptr = torch.cuda.current_stream().cuda_stream
+    L.check(lib.hn_quantize_rows_fp8(x.data_ptr(), NS_M, NS_K, NS_K, L.HN_SCALE_CLAMP, 1e-4,
+                                     qx_buf.data_ptr(), sx_buf.data_ptr(), stream_ptr),
+            "hn_quantize_rows_fp8")
+    ms_quant = time_loop(lambda: lib.hn_quantize_rows_fp8(
+        x.data_ptr(), NS_M, NS_K, NS_K, L.HN_SCALE_CLAMP, 1e-4, qx_buf.data_ptr(),
+        sx_buf.data_ptr(), stream_ptr), args.steps, args.warmup)
     f_ns = gemm_flops(NS_M, NS_K, NS_N)
     linear_tflops = f_ns / (ms_linear * 1e-3) / 1e12
     gemm_tflops = f_ns / (ms_gemm * 1e-3) / 1e12
@@ -144,8 +157,12 @@ def main():
     cache = kvc.make_fp8_kv_block(1, ATT_CHUNKS * KV_L, KV_H, KV_D, device=dev)
     kt, vt = k.transpose(1, 2), v.transpose(1, 2)        # [1, L, H, D] views of BHSD data
     slot = (ATT_CHUNKS - 1) * KV_L
-    kv_fn = lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"], cache["v_scale"], kt, vt, slot)
-    ms_kv = time_loop(kv_fn, args.steps, args.warmup)
+    kv_args = (L.HN_KV_FP8, kt.data_ptr(), vt.data_ptr(), L.strides(kt), 1, KV_L, KV_H, KV_D,
+               cache["k"].data_ptr(), cache["v"].data_ptr(), L.strides(cache["k"]),
+               cache["k_scale"].data_ptr(), cache["v_scale"].data_ptr(), L.strides(cache["k_scale"]),
+               slot, stream_ptr)
+    L.check(lib.hn_kv_quantize_pair(*kv_args), "hn_kv_quantize_pair")
+    ms_kv = time_loop(lambda: lib.hn_kv_quantize_pair(*kv_args), args.steps, args.warmup)
     kv_gbs = kv_write_bytes() / (ms_kv * 1e-3) / 1e9
     log(f"KV write {ms_kv * 1e3:.1f} us ({kv_gbs:.0f} GB/s)")
 

@@ -29,6 +29,18 @@ inline int check_launch(const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Compute units of the current device (256 if the query fails).
+int device_cus();
+
+// Grid for the streaming kernels' grid-stride loops: `per_cu` workgroups per
+// CU, fewer when there is less work. A moderate resident grid walking the
+// data in order sustains more HBM bandwidth on a mixed read/write stream than
+// one short-lived workgroup per unit of work.
+inline int64_t stream_grid(int64_t units, int per_cu) {
+    const int64_t g = (int64_t)device_cus() * per_cu;
+    return units < g ? units : g;
+}
+
 }  // namespace hn
 
 #define HN_REQUIRE(cond, code, msg) \

@@ -54,23 +54,30 @@ HN_DEVICE uint2 encode8(const uint4& v, const Quot& d) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-row quantization. One 256-thread block per row; each thread keeps up to
-// CPT chunks of 8 bf16 in registers between the amax pass and the encode pass,
-// so the row is read from HBM exactly once.
-template <int CPT>
+// Per-row quantization. One wave per row, four rows per 256-thread block: the
+// row max is a wave reduction (no block barrier), and each lane keeps its CPL
+// chunks of 8 bf16 in registers between the max and the encode pass, so the
+// row is read from HBM once with all of a lane's 16-byte loads in flight.
+template <int CPL>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
-    const uint16_t* __restrict__ x, int64_t cols, int64_t row_stride, int mode,
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t row_stride, int mode,
     float amax_floor, uint8_t* __restrict__ q, float* __restrict__ scale) {
-    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+         row += (int64_t)gridDim.x * 4) {  // grid-stride; whole waves, no barrier
     const uint16_t* xr = x + row * row_stride;
     const int nchunks = (int)(cols >> 3);
-    uint4 v[CPT];
+    uint4 v[CPL];
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        const int c = threadIdx.x + i * 256;
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane + i * 64;
+        if (c < nchunks) v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane + i * 64;
         if (c < nchunks) {
-            v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
             const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -80,21 +87,16 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
         }
     }
     amax = group_max<64>(amax);
-    __shared__ float red[4];
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float s = mode == HN_SCALE_CLAMP ? fmaxf(amax, amax_floor) / kE4M3Max
                                            : (amax > 0.0f ? amax / kE4M3Max : 1.0f);
-    if (threadIdx.x == 0) scale[row] = s;
+    if (lane == 0) scale[row] = s;
     const Quot d(s);
     uint8_t* qr = q + row * cols;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-        const int c = threadIdx.x + i * 256;
-        if (c < nchunks) {
-            *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8(v[i], d);
-        }
+    for (int i = 0; i < CPL; ++i) {
+        const int c = lane + i * 64;
+        if (c < nchunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8(v[i], d);
+    }
     }
 }
 
@@ -157,6 +159,11 @@ struct KvArgs {
     int64_t qs0, qs1, qs2;
     int64_t ss0, ss1, ss2;
     int64_t L, H, rows, start;
+    // Work units of KV_UNIT rows: TOKEN_FAST, KV_UNIT tokens of one (batch,
+    // head) (tiles = ceil(L / KV_UNIT) per head); otherwise KV_UNIT consecutive
+    // (token, head) rows of one batch (tiles = ceil(L * H / KV_UNIT) per batch,
+    // L * H < 2^31).
+    int64_t tiles, units;
 };
 
 HN_DEVICE uint32_t int8_code(float v) {
@@ -168,23 +175,43 @@ HN_DEVICE uint32_t int8_code(float v) {
 }
 
 constexpr int KV_ROWS_PER_GROUP = 4;  // rows each 16-lane group carries (loads issued together)
+constexpr int KV_UNIT = 16 * KV_ROWS_PER_GROUP;
 
-template <int FMT>
+// TOKEN_FAST: rows are enumerated token-fastest within a (batch, head) instead
+// of head-fastest, chosen when the values' token stride is the smaller one (a
+// [B, H, L, D] source viewed as [B, L, H, D]): the loads of consecutive rows
+// are then consecutive 256-byte rows of the source, and each 128-byte code row
+// is still one whole cache line.
+template <int FMT, bool TOKEN_FAST>
 __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
     const int sel = blockIdx.y;
     const int lane16 = threadIdx.x & 15;
-    // The 16 groups of a block take interleaved rows so that, for each of the
-    // KV_ROWS_PER_GROUP steps, the block covers 16 consecutive rows.
-    const int64_t base = (int64_t)blockIdx.x * 16 * KV_ROWS_PER_GROUP + (threadIdx.x >> 4);
+    for (int64_t unit = blockIdx.x; unit < a.units; unit += gridDim.x) {  // grid-stride
+    // The unit's rows: group g (16 lanes) takes rows g + 16 k, so for
+    // each k the block covers 16 consecutive rows. Unit -> (batch, head or row
+    // tile) is one wave-uniform division; per row there is none on the
+    // TOKEN_FAST path and one 32-bit division by H otherwise.
+    const int g = threadIdx.x >> 4;
+    const int64_t outer = unit / a.tiles;      // TOKEN_FAST: b * H + h; else b
+    const int64_t tile = unit - outer * a.tiles;
     uint4 v[KV_ROWS_PER_GROUP];
     int64_t rb[KV_ROWS_PER_GROUP], rt[KV_ROWS_PER_GROUP], rh[KV_ROWS_PER_GROUP];
 #pragma unroll
     for (int k = 0; k < KV_ROWS_PER_GROUP; ++k) {
-        int64_t row = base + k * 16;
-        row = row < a.rows ? row : a.rows - 1;  // duplicates of the last row rewrite identical bytes
-        rh[k] = row % a.H;
-        rt[k] = (row / a.H) % a.L;
-        rb[k] = row / (a.H * a.L);
+        // Rows past the end repeat the last row: they rewrite identical bytes.
+        if (TOKEN_FAST) {
+            const int64_t t = tile * KV_UNIT + g + 16 * k;
+            rb[k] = outer / a.H;
+            rh[k] = outer - rb[k] * a.H;
+            rt[k] = t < a.L ? t : a.L - 1;
+        } else {
+            int64_t r = tile * KV_UNIT + g + 16 * k;
+            r = r < a.L * a.H ? r : a.L * a.H - 1;
+            const uint32_t t = (uint32_t)r / (uint32_t)a.H;
+            rb[k] = outer;
+            rt[k] = t;
+            rh[k] = r - (int64_t)t * a.H;
+        }
         v[k] = *reinterpret_cast<const uint4*>(a.x[sel] + rb[k] * a.xs0 + rt[k] * a.xs1 +
                                                rh[k] * a.xs2 + lane16 * 8);
     }
@@ -220,6 +247,7 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
         *reinterpret_cast<uint2*>(a.q[sel] + rb[k] * a.qs0 + tt * a.qs1 + rh[k] * a.qs2 + lane16 * 8) =
             make_uint2(lo, hi);
         if (lane16 == 0) a.s[sel][rb[k] * a.ss0 + tt * a.ss1 + rh[k] * a.ss2] = s;
+    }
     }
 }
 
@@ -287,29 +315,28 @@ extern "C" int hn_quantize_rows_fp8(const void* x, int64_t rows, int64_t cols,
     if (rows == 0) return HN_OK;
     HN_REQUIRE(x && q && scale, HN_E_ARG, "hn_quantize_rows_fp8: null pointer");
     HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_quantize_rows_fp8: too many rows");
-    const int chunks_per_thread = (int)((cols / 8 + 255) / 256);
-    const dim3 grid((unsigned)rows);
+    const int per_lane = (int)((cols / 8 + 63) / 64);  // 16-byte chunks per lane, <= 32
+    const dim3 grid((unsigned)stream_grid((rows + 3) / 4, 8));
     hipStream_t st = (hipStream_t)stream;
     const uint16_t* xp = (const uint16_t*)x;
     uint8_t* qp = (uint8_t*)q;
-#define HN_ROWS_CASE(N)                                                                   \
-    case N:                                                                               \
-        quantize_rows_kernel<N><<<grid, 256, 0, st>>>(xp, cols, row_stride, scale_mode,  \
-                                                      amax_floor, qp, scale);             \
-        break;
-    switch (chunks_per_thread) {
-        HN_ROWS_CASE(1)
-        HN_ROWS_CASE(2)
-        HN_ROWS_CASE(3)
-        HN_ROWS_CASE(4)
-        HN_ROWS_CASE(5)
-        HN_ROWS_CASE(6)
-        HN_ROWS_CASE(7)
-        HN_ROWS_CASE(8)
-        default:
-            return fail(HN_E_ARG, "hn_quantize_rows_fp8: unsupported width");
+#define HN_ROWS_CASE(N)                                                                       \
+    if (per_lane <= N) {                                                                      \
+        quantize_rows_kernel<N><<<grid, 256, 0, st>>>(xp, rows, cols, row_stride, scale_mode, \
+                                                      amax_floor, qp, scale);                 \
+        return check_launch("hn_quantize_rows_fp8");                                          \
     }
+    HN_ROWS_CASE(1)
+    HN_ROWS_CASE(2)
+    HN_ROWS_CASE(4)
+    HN_ROWS_CASE(6)
+    HN_ROWS_CASE(8)
+    HN_ROWS_CASE(12)
+    HN_ROWS_CASE(16)
+    HN_ROWS_CASE(24)
+    HN_ROWS_CASE(32)
 #undef HN_ROWS_CASE
+    return fail(HN_E_ARG, "hn_quantize_rows_fp8: unsupported width");
     return check_launch("hn_quantize_rows_fp8");
 }
 
@@ -356,13 +383,18 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
     a.qs0 = qs[0]; a.qs1 = qs[1]; a.qs2 = qs[2];
     a.ss0 = ss[0]; a.ss1 = ss[1]; a.ss2 = ss[2];
     a.L = L; a.H = H; a.rows = rows; a.start = start;
-    const int64_t blocks = (rows + 16 * KV_ROWS_PER_GROUP - 1) / (16 * KV_ROWS_PER_GROUP);
-    HN_REQUIRE(blocks <= 0x7fffffffLL, HN_E_ARG, "KV write too large");
-    const dim3 grid((unsigned)blocks, (unsigned)n);
-    if (fmt == HN_KV_FP8)
-        kv_quantize_kernel<HN_KV_FP8><<<grid, 256, 0, (hipStream_t)stream>>>(a);
-    else
-        kv_quantize_kernel<HN_KV_INT8><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    const bool token_fast = xs[1] < xs[2];
+    HN_REQUIRE(token_fast || L * H < 0x7fffffffLL, HN_E_ARG, "KV write: too many rows per batch");
+    a.tiles = token_fast ? (L + KV_UNIT - 1) / KV_UNIT : (L * H + KV_UNIT - 1) / KV_UNIT;
+    a.units = (token_fast ? B * H : B) * a.tiles;
+    const dim3 grid((unsigned)stream_grid(a.units, 16 / n), (unsigned)n);
+    if (fmt == HN_KV_FP8) {
+        if (token_fast) kv_quantize_kernel<HN_KV_FP8, true><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+        else kv_quantize_kernel<HN_KV_FP8, false><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    } else {
+        if (token_fast) kv_quantize_kernel<HN_KV_INT8, true><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+        else kv_quantize_kernel<HN_KV_INT8, false><<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    }
     return check_launch(who);
 }
 
