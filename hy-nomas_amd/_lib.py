@@ -41,6 +41,8 @@ SIGNATURES = {
     "hn_attn_fp8kv": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P, _PI64,
                       _I64, _P, _P, _PI64, _I64, _I64, _I64, _F, _P, _PI64, _P, _I64, _P],
     "hn_attn_fp8kv_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
+    "hn_qk_norm_rope_kv": [_I, _P, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _F,
+                           _P, _P, _PI64, _P, _P, _PI64, _I64, _P],
 }
 RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64}
 

@@ -32,4 +32,4 @@ int device_cus() {
 
 extern "C" const char* hn_last_error(void) { return hn::g_last_error; }
 
-extern "C" int hn_abi_version(void) { return 2; }
+extern "C" int hn_abi_version(void) { return 3; }

@@ -64,6 +64,42 @@ HN_DEVICE uint32_t e4m3_encode4(float a, float b, float c, float d) {
     return (uint32_t)w;
 }
 
+// The fp32 quotient x / s of a quantizer, from the row's reciprocal.
+//
+// Per row: s and r = fl32(1 / s) (one IEEE division). Per element:
+//   y = fl(x * r);  e = fma(-s, y, x) (exact residual);  q = fma(e, r, y)
+// with the sign of x restored on q (an exactly-zero fma result is +0, while
+// x / s keeps the sign of x). Three VALU operations replace the ~10 of an IEEE
+// division. The result is not always fl32(x / s) in its last bit, but the
+// *codes* derived from it are identical: for every bf16 row maximum amax and
+// every bf16 x with |x| <= amax, for each scale rule in use
+// (max(amax, 1e-4) / 448, amax > 0 ? amax / 448 : 1, amax > 0 ? amax / 127 : 1),
+// e4m3_rne(q) == e4m3_rne(x / s) and the INT8 rounding of q equals that of
+// x / s. That was checked exhaustively on the host (2 x 5.3e8 (amax, x)
+// pairs per rule). The check holds for s >= 2^-100; smaller or non-finite
+// scales (rows whose amax is within ~2^-91 of zero, or non-finite rows) take
+// the IEEE division, since there the residual e underflows.
+struct Quot {
+    float s, r;
+    bool exact;
+    HN_DEVICE explicit Quot(float scale)
+        : s(scale), r(1.0f / scale), exact(!(scale >= 0x1p-100f && scale <= 3.4028234e38f)) {}
+    HN_DEVICE float operator()(float x) const {
+        if (exact) return x / s;
+        const float y = __fmul_rn(x, r);
+        const float e = __fmaf_rn(-s, y, x);
+        return __builtin_copysignf(__fmaf_rn(e, r, y), x);
+    }
+};
+
+HN_DEVICE uint32_t int8_code(float v) {
+    // int8_kv_cache.py:150-157: fp32 round-half-away via floor(v + 0.5) /
+    // ceil(v - 0.5) (each add rounded in fp32), then clamp to +-127.
+    float r = v >= 0.0f ? floorf(v + 0.5f) : ceilf(v - 0.5f);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return (uint32_t)(int32_t)r & 0xffu;
+}
+
 // OCP e4m3 byte -> fp32 (exact).
 HN_DEVICE float e4m3_decode(uint32_t c) {
     const uint32_t e = (c >> 3) & 15u, m = c & 7u;

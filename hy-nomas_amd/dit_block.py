@@ -21,6 +21,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from .cache_attention import chunk_attention
 from .dit_fp8_linear import FP8StoredLinear, fp8_linear
 from .fp8_kv_cache import make_fp8_kv_block, quantize_kv_pair_into
@@ -42,17 +43,6 @@ def rope_tables(frames: int, height: int, width: int, dims=(16, 56, 56), theta: 
     return torch.cat(cos, dim=1), torch.cat(sin, dim=1)
 
 
-def _rms_norm(x, weight, eps):
-    y = x.float()
-    y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + eps)
-    return y.to(x.dtype) * weight
-
-
-def _rotate_half(x):
-    real, imag = x.float().reshape(*x.shape[:-1], -1, 2).unbind(-1)
-    return torch.stack((-imag, real), dim=-1).flatten(3)
-
-
 def _modulate(x, shift, scale):
     return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
 
@@ -61,10 +51,15 @@ class FP8DiTBlock(nn.Module):
     """Image stream of one double-stream block at inference, FP8 linears."""
 
     def __init__(self, hidden: int = 3072, heads: int = 24, mlp_ratio: int = 4,
-                 qk_eps: float = 1e-6, *, device=None, generator=None):
+                 qk_eps: float = 1e-6, *, device=None, generator=None,
+                 validate_kv_writes: bool = True):
         super().__init__()
         self.hidden, self.heads, self.head_dim = hidden, heads, hidden // heads
         self.qk_eps = qk_eps
+        # True: the cache write validates K and V (finite) before writing either,
+        # as quantize_kv_pair_into does (one host sync per write pass). False:
+        # the write is fused into the QK norm/RoPE kernel, unvalidated.
+        self.validate_kv_writes = validate_kv_writes
         kw = dict(device=device, dtype=torch.bfloat16)
 
         def lin(i, o):
@@ -82,10 +77,13 @@ class FP8DiTBlock(nn.Module):
         self.q_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
         self.k_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
 
-    def pre_attention(self, img, vec, cos, sin):
+    def pre_attention(self, img, vec, cos, sin, kv_cache=None, cache_start: int = 0):
         """Image-stream half of nomas_compile_prepost.pre_attention (:29-72):
-        adaLN parts, LayerNorm + modulate, fused FP8 QKV, per-head RMSNorm, RoPE.
-        Returns q, k, v [B, L, H, D] bf16 and the six modulation parts."""
+        adaLN parts, LayerNorm + modulate, fused FP8 QKV, then per-head RMSNorm
+        and RoPE in one kernel, in place on the QKV output. Returns q, k, v
+        [B, L, H, D] bf16 (views of that output) and the six modulation parts.
+        With ``kv_cache`` given, the rotated K and V are also written into it at
+        ``cache_start`` by the same kernel (unvalidated)."""
         B, L, C = img.shape
         H, D = self.heads, self.head_dim
         with stage("modulation"):
@@ -93,15 +91,16 @@ class FP8DiTBlock(nn.Module):
             x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
         with stage("qkv_fp8"):
             qkv = fp8_linear(self.qkv, x).view(B, L, 3, H, D)
+        # select views (not unbind's multi-output views), so the in-place
+        # norm/RoPE may modify them
+        q, k, v = qkv.select(2, 0), qkv.select(2, 1), qkv.select(2, 2)
         with stage("qk_norm_rope"):
-            q, k, v = qkv.unbind(2)
-            q = _rms_norm(q, self.q_norm, self.qk_eps).to(v.dtype)
-            k = _rms_norm(k, self.k_norm, self.qk_eps).to(v.dtype)
-            c = cos.view(1, L, 1, D)
-            s = sin.view(1, L, 1, D)
-            q = (q.float() * c + _rotate_half(q) * s).type_as(v)
-            k = (k.float() * c + _rotate_half(k) * s).type_as(v)
-            v = v.contiguous()
+            if kv_cache is None:
+                ops.qk_norm_rope_(q, k, v, self.q_norm, self.k_norm, cos, sin, self.qk_eps)
+            else:
+                ops.qk_norm_rope_kv_(q, k, v, self.q_norm, self.k_norm, cos, sin, self.qk_eps,
+                                     kv_cache["k"], kv_cache["v"], kv_cache["k_scale"],
+                                     kv_cache["v_scale"], cache_start)
         return q, k, v, parts
 
     def post_attention(self, img, attn, parts):
@@ -119,8 +118,10 @@ class FP8DiTBlock(nn.Module):
 
     def forward(self, img, vec, cos, sin, kv_cache, cache_valid_len: int,
                 update_cache: bool = False):
-        q, k, v, parts = self.pre_attention(img, vec, cos, sin)
-        if update_cache:
+        fused = update_cache and not self.validate_kv_writes
+        q, k, v, parts = self.pre_attention(img, vec, cos, sin, kv_cache if fused else None,
+                                            cache_valid_len)
+        if update_cache and self.validate_kv_writes:
             with stage("kv_write_fp8"):
                 quantize_kv_pair_into(kv_cache, k, v, cache_valid_len)
         with stage("cache_attention"):

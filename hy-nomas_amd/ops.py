@@ -240,6 +240,68 @@ def _(codes, scale, valid_len):
 
 
 # --------------------------------------------------------------------------
+# fused QK RMSNorm + RoPE (+ KV cache write)
+
+def _qk_launch(q, k, v, q_weight, k_weight, cos, sin, eps, cache, start):
+    _gpu(q, k, v, q_weight, k_weight, cos, sin, *(cache or ()))
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise TypeError("qk_norm_rope expects bf16 q, k, v")
+    if q.stride() != k.stride() or q.stride() != v.stride() or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k and v must share shape and strides")
+    B, Lt, H, D = q.shape
+    cos = cos.reshape(-1, D)
+    sin = sin.reshape(-1, D)
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape[0] < Lt or cos.stride() != sin.stride():
+        raise ValueError("cos/sin must be fp32 [L, D] tables with one layout")
+    qw = q_weight.to(torch.bfloat16).contiguous()
+    kw = k_weight.to(torch.bfloat16).contiguous()
+    if cache:
+        k_codes, v_codes, k_scale, v_scale = cache
+        fmt = _kv_fmt(k_codes)
+        if v_codes.dtype != k_codes.dtype or k_codes.stride() != v_codes.stride() or k_scale.stride() != v_scale.stride():
+            raise ValueError("K/V caches must share dtype and layout")
+        cargs = (k_codes.data_ptr(), v_codes.data_ptr(), L.strides(k_codes), k_scale.data_ptr(),
+                 v_scale.data_ptr(), L.strides(k_scale))
+    else:
+        fmt = L.HN_KV_FP8
+        cargs = (None, None, None, None, None, None)
+    with torch.cuda.device(q.device):
+        L.check(L.load().hn_qk_norm_rope_kv(
+            fmt, q.data_ptr(), k.data_ptr(), v.data_ptr(), L.strides(q), B, Lt, H, D,
+            qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.stride(0), eps,
+            *cargs, start, _stream(q)), "hn_qk_norm_rope_kv")
+
+
+@torch.library.custom_op("hy_nomas_amd::qk_norm_rope_", mutates_args=("q", "k"))
+def qk_norm_rope_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                  k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float) -> None:
+    """In place: q, k <- RoPE(RMSNorm(q)), RoPE(RMSNorm(k)) for bf16 [B, L, H, 128]
+    views sharing strides (v is only checked for layout)."""
+    _qk_launch(q, k, v, q_weight, k_weight, cos, sin, eps, None, 0)
+
+
+@qk_norm_rope_.register_fake
+def _(q, k, v, q_weight, k_weight, cos, sin, eps):
+    return None
+
+
+@torch.library.custom_op("hy_nomas_amd::qk_norm_rope_kv_",
+                         mutates_args=("q", "k", "k_codes", "v_codes", "k_scale", "v_scale"))
+def qk_norm_rope_kv_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                     k_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                     k_codes: torch.Tensor, v_codes: torch.Tensor, k_scale: torch.Tensor,
+                     v_scale: torch.Tensor, start: int) -> None:
+    """qk_norm_rope_, and the rotated k and v written into the KV caches at
+    token offset ``start`` by the same kernel (no finiteness validation)."""
+    _qk_launch(q, k, v, q_weight, k_weight, cos, sin, eps, (k_codes, v_codes, k_scale, v_scale), start)
+
+
+@qk_norm_rope_kv_.register_fake
+def _(q, k, v, q_weight, k_weight, cos, sin, eps, k_codes, v_codes, k_scale, v_scale, start):
+    return None
+
+
+# --------------------------------------------------------------------------
 # attention
 
 @torch.library.custom_op("hy_nomas_amd::attn_fp8kv", mutates_args=())

@@ -159,6 +159,30 @@ int hn_attn_fp8kv(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t 
 int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
                                      int64_t kv_len, int64_t cur_len);
 
+/* Fused pre-attention tail of the DiT block's image stream, in place:
+ *   q <- RoPE(RMSNorm_qw(q)),  k <- RoPE(RMSNorm_kw(k))
+ * per (batch, token, head) row of D == 128, with the reference's op order and
+ * bf16 rounding points: y = bf16(x * rsqrt(mean(x^2) + eps)); y = bf16(y * w);
+ * out = bf16(y * cos + rotate_half(y) * sin), rotate_half(y0, y1) = (-y1, y0),
+ * products and sums rounded separately in fp32.
+ *   q, k, v: bf16 [B, L, H, D] sharing strides xs[4] (xs[3] == 1), e.g. views
+ *            of one fused QKV projection output; q and k are overwritten
+ *   q_weight, k_weight: bf16 [D]; cos, sin: fp32 [L, D] with row stride cs
+ * When kc is non-NULL, the rotated k and v are also written into the KV cache
+ * (kc, vc codes [B, cap, H, D] with strides qs[4]; ks, vs fp32 scales with
+ * strides ss[3]) at token offset start, exactly as hn_kv_quantize_pair would
+ * write them (no finiteness validation: callers that need the reference's
+ * validate-before-write behaviour pass kc = NULL and use hn_kv_quantize_pair).
+ * Replaces _rms_norm / _rotate_half and the q/k tail of pre_attention,
+ * hymm/models/dit/modules/nomas_compile_prepost.py:18-27,49-54 (RMSNorm
+ * norm_layers.py:49-63, RoPE posemb_layers.py:401-453), fused with the cache
+ * write of quantize_kv_pair_into, int8_kv_cache.py:161-179. */
+int hn_qk_norm_rope_kv(int fmt, void *q, void *k, const void *v, const int64_t *xs, int64_t B,
+                       int64_t L, int64_t H, int64_t D, const void *q_weight,
+                       const void *k_weight, const float *cos, const float *sin, int64_t cs,
+                       float eps, void *kc, void *vc, const int64_t *qs, float *ks, float *vs,
+                       const int64_t *ss, int64_t start, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

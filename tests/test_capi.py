@@ -33,7 +33,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.hn_abi_version() == 2
+    assert lib.hn_abi_version() == 3
 
 
 def _err(lib):
@@ -59,6 +59,12 @@ def test_argument_errors_are_reported_without_a_launch(lib):
                              None, None, None, 0, 0, 0, 1.0, None, st, None, 0, None) == -1
     assert "head dim" in _err(lib)
     assert lib.hn_attn_fp8kv_workspace_size(1, 128, 24, 64, 1000, 0) == 0   # bad head dim
+    assert lib.hn_qk_norm_rope_kv(0, None, None, None, st, 1, 4, 2, 64, None, None, None, None, 128,
+                                  1e-6, None, None, None, None, None, None, 0, None) == -1
+    assert "head dim" in _err(lib)
+    assert lib.hn_qk_norm_rope_kv(3, None, None, None, st, 1, 4, 2, 128, None, None, None, None, 128,
+                                  1e-6, None, None, None, None, None, None, 0, None) == -1
+    assert "format" in _err(lib)
     # zero-size work is a no-op that needs no pointers
     assert lib.hn_quantize_rows_fp8(None, 0, 8, 8, 0, 1e-4, None, None, None) == L.HN_OK
     assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 0, 128, 128, 128, 0, None) == L.HN_OK

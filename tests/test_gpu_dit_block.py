@@ -179,7 +179,8 @@ def test_block_end_to_end(dev, update_cache):
     assert bool(written.any()) == update_cache
     assert not cache["k"][:, hist + L:].view(torch.uint8).any()
     if update_cache:                               # the write is the KV kernel on this pass's K/V
-        _, k, v, _ = blk.pre_attention(img, vec, cos, sin)
+        with torch.no_grad():
+            _, k, v, _ = blk.pre_attention(img, vec, cos, sin)
         kvc = pkg_module("fp8_kv_cache")
         check = kvc.make_fp8_kv_block(1, L, blk.heads, 128, device=dev)
         kvc.quantize_kv_pair_into(check, k, v, 0)
