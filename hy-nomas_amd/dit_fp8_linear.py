@@ -50,6 +50,26 @@ class FP8StoredLinear(nn.Module):
         self.register_buffer("weight_scale", s)
         self.bias = original.bias
 
+    @classmethod
+    def from_codes(cls, weight_q: torch.Tensor, weight_scale: torch.Tensor,
+                   bias: torch.Tensor | None = None) -> "FP8StoredLinear":
+        """A layer from e4m3 codes [out, in] and fp32 per-channel scales [out]
+        (e.g. requantized from a W8 checkpoint)."""
+        out_f, in_f = weight_q.shape
+        if weight_q.dtype != torch.float8_e4m3fn or weight_scale.dtype != torch.float32:
+            raise TypeError("Expected float8_e4m3fn codes and float32 scales")
+        if in_f % 128 or out_f % 128 or tuple(weight_scale.reshape(-1).shape) != (out_f,):
+            raise ValueError("FP8 linear needs in/out features divisible by 128 and one scale per output")
+        if not torch.isfinite(weight_scale).all() or not (weight_scale > 0).all():
+            raise ValueError("FP8 scales must be finite and positive")
+        m = cls.__new__(cls)
+        nn.Module.__init__(m)
+        m.in_features, m.out_features = in_f, out_f
+        m.register_buffer("weight_q", weight_q)
+        m.register_buffer("weight_scale", weight_scale.reshape(-1))
+        m.bias = None if bias is None else nn.Parameter(bias.to(torch.bfloat16), requires_grad=False)
+        return m
+
     def dequant_weight(self) -> torch.Tensor:
         return (self.weight_q.float() * self.weight_scale[:, None]).to(torch.bfloat16)
 
