@@ -79,7 +79,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "copy"])
+    ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
+    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "copy", "ar"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -102,6 +103,9 @@ def main():
         dst = torch.empty_like(src)
         ms = time_loop(lambda: dst.copy_(src), args.steps, args.warmup)
         log(f"copy 1 GiB: {ms:.3f} ms ({2 * (1 << 30) / (ms * 1e-3) / 1e9:.0f} GB/s read+write)")
+        return
+    if args.only == "ar":
+        print(json.dumps(bench_ar(args, torch, ops, dev, log)))
         return
     if args.only != "all":
         return run_only(args, torch, ops, kvc, ca, dev, log)
@@ -190,6 +194,9 @@ def main():
     blk_res = bench_block(args, torch, cache, dev, g, log)
     del cache, q, qd
 
+    # ---------------- config 5: 40-block AR chunk at the largest cache
+    ar_res = bench_ar(args, torch, ops, dev, log) if not args.no_ar else None
+
     # ---------------- CPU baseline: the oracle's dequantize-then-matmul
     cpu = None
     if not args.no_cpu_baseline:
@@ -238,6 +245,7 @@ def main():
                       "decode_lq128_gbs": round(dec_gbs, 1),
                       "decode_frac_hbm": round(dec_gbs / HBM_PEAK_GBS, 4)},
         "dit_block": blk_res,
+        "ar_chunk": ar_res,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
@@ -271,6 +279,52 @@ def bench_block(args, torch, cache, dev, g, log):
     return {"ms": round(ms, 4), "tflops": round(tflops, 2), "linear_tflop": round(lin / 1e12, 4),
             "attention_tflop": round(att / 1e12, 4), "stage_ms": stages,
             "shape": {"tokens": KV_L, "hidden": 3072, "heads": KV_H, "cached_tokens": hist}}
+
+
+def ar_chunk_flops(depth=40, prior=16, hidden=3072, heads=24, tokens=KV_L, d=KV_D, passes=5):
+    """One AR chunk: `passes` passes of `depth` blocks, each block's linears plus
+    attention over `prior` cached chunks and the current chunk."""
+    lin, att = block_flops(hidden, heads, tokens, (prior + 1) * tokens, d)
+    return passes * depth * (lin + att)
+
+
+def bench_ar(args, torch, ops, dev, log):
+    """Config 5: the 40-block AR step at the largest cache -- 4 denoising passes
+    and 1 cache-write pass over 16 prior chunks (172 800 cached tokens per
+    layer, FP8 codes written by the KV-write kernel)."""
+    db = importlib.import_module("hy-nomas_amd.dit_block")
+    depth, prior = 40, 16
+    model = db.FP8ARModel(depth=depth, device=dev, seed=7)
+    g = torch.Generator(device=dev).manual_seed(99)
+    k = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+    for cache in model.caches:
+        for c in range(prior):
+            ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"], cache["v_scale"],
+                                  k, v, c * KV_L)
+    del k, v
+    model.cache_valid_len = prior * KV_L
+    model.frames_done = prior * model.latent_shape[0]
+    noise = torch.randn(1, KV_L, 3072, device=dev, generator=g).to(torch.bfloat16)
+    vecs = [torch.randn(1, 3072, device=dev, generator=g).to(torch.bfloat16) for _ in range(5)]
+    sigmas = torch.linspace(1.0, 0.0, 5).tolist()
+    with torch.no_grad():
+        model.forward_chunk(noise, vecs[0], update_cache=False)    # warm-up pass
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.generate_chunk(noise, vecs[:4], vecs[4], sigmas)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+    flops = ar_chunk_flops(depth, prior)
+    frames = model.latent_shape[0]
+    log(f"config-5 AR chunk ({depth} blocks, {prior} prior chunks, 4+1 passes): {sec * 1e3:.0f} ms, "
+        f"{frames / sec:.3f} latent frames/s, {flops / sec / 1e12:.0f} TFLOP/s")
+    del model
+    torch.cuda.empty_cache()
+    return {"ms_per_chunk": round(sec * 1e3, 1), "latent_frames_per_s": round(frames / sec, 4),
+            "tflops": round(flops / sec / 1e12, 1), "pflop_per_chunk": round(flops / 1e15, 3),
+            "shape": {"blocks": depth, "prior_chunks": prior, "passes": "4 denoise + 1 cache write",
+                      "tokens_per_chunk": KV_L, "cache_tokens_per_layer": prior * KV_L}}
 
 
 def run_only(args, torch, ops, kvc, ca, dev, log):
