@@ -339,10 +339,12 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
         ms = time_loop(lambda: ops.gemm_fp8_rowcol(qx, qw, sx, sw, bias, 1), args.steps, args.warmup)
         log(f"north-star GEMM {ms:.3f} ms")
     elif args.only == "kv":
-        k = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+        # the config-2 layout of the main run: [1, H, L, D] data viewed as [1, L, H, D]
+        k = torch.randn(1, KV_H, KV_L, KV_D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
+        v = torch.randn(1, KV_H, KV_L, KV_D, device=dev, generator=g).to(torch.bfloat16).transpose(1, 2)
         cache = kvc.make_fp8_kv_block(1, KV_L, KV_H, KV_D, device=dev)
         ms = time_loop(lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"],
-                                                     cache["v_scale"], k, k, 0), args.steps, args.warmup)
+                                                     cache["v_scale"], k, v, 0), args.steps, args.warmup)
         log(f"KV write {ms * 1e3:.1f} us")
     elif args.only == "attn":
         lk = ATT_CHUNKS * KV_L
