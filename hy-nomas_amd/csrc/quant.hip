@@ -131,11 +131,11 @@ struct KvArgs {
     int64_t qs0, qs1, qs2;
     int64_t ss0, ss1, ss2;
     int64_t L, H, rows, start;
-    // Work units of KV_UNIT rows: TOKEN_FAST, KV_UNIT tokens of one (batch,
-    // head) (tiles = ceil(L / KV_UNIT) per head); otherwise KV_UNIT consecutive
-    // (token, head) rows of one batch (tiles = ceil(L * H / KV_UNIT) per batch,
-    // L * H < 2^31).
-    int64_t tiles, units;
+    // Work units of KV_UNIT = 64 rows. TOKEN_FAST: 8 tokens x 8 heads of one
+    // batch (ttiles = ceil(L / 8) token tiles per head tile, htiles =
+    // ceil(H / 8)); otherwise 64 consecutive (token, head) rows of one batch
+    // (ttiles = ceil(L * H / 64) per batch, L * H < 2^31).
+    int64_t ttiles, htiles, units;
 };
 
 constexpr int KV_ROWS_PER_GROUP = 4;  // rows each 16-lane group carries (loads issued together)
@@ -151,28 +151,34 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
     const int sel = blockIdx.y;
     const int lane16 = threadIdx.x & 15;
     for (int64_t unit = blockIdx.x; unit < a.units; unit += gridDim.x) {  // grid-stride
-    // The unit's rows: group g (16 lanes) takes rows g + 16 k, so for
-    // each k the block covers 16 consecutive rows. Unit -> (batch, head or row
-    // tile) is one wave-uniform division; per row there is none on the
-    // TOKEN_FAST path and one 32-bit division by H otherwise.
+    // Group g (16 lanes) takes 4 rows, k = 0..3. TOKEN_FAST: token 8 tt + g % 8
+    // of heads 8 ht + 4 (g / 8) + k -- for each k the loads are two runs of 8
+    // consecutive tokens (2 KB each), and every token's 8 heads of codes
+    // (1 KB) and scales (one 32-byte sector) are written by the unit.
+    // Otherwise rows g + 16 k of the unit's 64 consecutive (token, head) rows.
+    // Unit -> tiles is one wave-uniform division; per row there is no
+    // division on the TOKEN_FAST path and one 32-bit division by H otherwise.
     const int g = threadIdx.x >> 4;
-    const int64_t outer = unit / a.tiles;      // TOKEN_FAST: b * H + h; else b
-    const int64_t tile = unit - outer * a.tiles;
     uint4 v[KV_ROWS_PER_GROUP];
     int64_t rb[KV_ROWS_PER_GROUP], rt[KV_ROWS_PER_GROUP], rh[KV_ROWS_PER_GROUP];
 #pragma unroll
     for (int k = 0; k < KV_ROWS_PER_GROUP; ++k) {
-        // Rows past the end repeat the last row: they rewrite identical bytes.
+        // Rows past the end repeat the last token / head: they rewrite identical bytes.
         if (TOKEN_FAST) {
-            const int64_t t = tile * KV_UNIT + g + 16 * k;
-            rb[k] = outer / a.H;
-            rh[k] = outer - rb[k] * a.H;
+            const int64_t bh = unit / a.ttiles;          // b * htiles + ht
+            const int64_t tt = unit - bh * a.ttiles;
+            const int64_t b = bh / a.htiles;
+            const int64_t t = tt * 8 + (g & 7);
+            const int64_t h = (bh - b * a.htiles) * 8 + 4 * (g >> 3) + k;
+            rb[k] = b;
             rt[k] = t < a.L ? t : a.L - 1;
+            rh[k] = h < a.H ? h : a.H - 1;
         } else {
-            int64_t r = tile * KV_UNIT + g + 16 * k;
+            const int64_t b = unit / a.ttiles;
+            int64_t r = (unit - b * a.ttiles) * KV_UNIT + g + 16 * k;
             r = r < a.L * a.H ? r : a.L * a.H - 1;
             const uint32_t t = (uint32_t)r / (uint32_t)a.H;
-            rb[k] = outer;
+            rb[k] = b;
             rt[k] = t;
             rh[k] = r - (int64_t)t * a.H;
         }
@@ -349,8 +355,10 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
     a.L = L; a.H = H; a.rows = rows; a.start = start;
     const bool token_fast = xs[1] < xs[2];
     HN_REQUIRE(token_fast || L * H < 0x7fffffffLL, HN_E_ARG, "KV write: too many rows per batch");
-    a.tiles = token_fast ? (L + KV_UNIT - 1) / KV_UNIT : (L * H + KV_UNIT - 1) / KV_UNIT;
-    a.units = (token_fast ? B * H : B) * a.tiles;
+    static_assert(KV_UNIT == 64, "token-fast units are 8 tokens x 8 heads");
+    a.htiles = token_fast ? (H + 7) / 8 : 1;
+    a.ttiles = token_fast ? (L + 7) / 8 : (L * H + KV_UNIT - 1) / KV_UNIT;
+    a.units = B * a.htiles * a.ttiles;
     const dim3 grid((unsigned)stream_grid(a.units, 16 / n), (unsigned)n);
     if (fmt == HN_KV_FP8) {
         if (token_fast) kv_quantize_kernel<HN_KV_FP8, true><<<grid, 256, 0, (hipStream_t)stream>>>(a);
