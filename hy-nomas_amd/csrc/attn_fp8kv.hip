@@ -3,28 +3,26 @@
 //   O = softmax(Q K^T * scale) V,   K, V = code * per-(token, head) scale
 //
 // Work decomposition: one workgroup = 4 waves = 128 queries of one (batch,
-// head); each wave owns 32 queries (one 32-column MFMA block), and two
-// workgroups share a CU (2 waves per SIMD), so one wave's softmax VALU work
-// overlaps the other's MFMAs. Keys stream
-// through LDS in tiles of 64. K codes are widened to bf16 once per workgroup
-// as they are written to LDS (exact: every e4m3 and int8 code is a bf16
-// value) and the per-token K scale (times softmax_scale * log2 e) multiplies
-// the fp32 logits, so K enters as code * scale in fp32. V codes are widened to
-// fp16 (also exact) and the per-token V scale multiplies the fp32 probability
-// before it is packed to fp16 for the PV MFMA: P' = fp16(p * s_v), so the PV
-// product carries fp16's 2^-11 relative rounding instead of bf16's 2^-8. The
-// optional unquantized tail (the current chunk's bf16 K/V) is copied into the
-// same LDS formats with unit scales, so one compute path serves both segments.
+// head); each wave owns 32 queries (one 32-column MFMA block); two workgroups
+// share a CU (2 waves per SIMD). Keys stream through LDS in tiles of 64, two
+// stages. Each tile is dequantized once per workgroup as it is written to LDS,
+// to the reference's own dequantized values: K = bf16(code * k_scale) and
+// V = bf16(code * v_scale) (fp32 product, rounded to nearest even), so the
+// MFMAs consume exactly the bf16 K/V the reference attends over, and no
+// per-key scale is needed in the compute loop. The optional unquantized tail
+// (the current chunk's bf16 K/V) is copied into the same LDS formats.
 //
-// Per tile the wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: the
-// MFMA output puts one query per lane column, so the online-softmax max/sum
-// are lane-local plus one exchange with lane ^ 32. P^T is packed to fp16 in
-// registers and reused as the B operand of O^T += V^T P^T on
-// v_mfma_f32_32x32x16_f16. V is stored in LDS in its natural [key][dim] order
-// and the V^T operand is fetched with gfx950's transposing LDS read
-// (ds_read_b64_tr_b16), in the key order of the S^T registers. Two LDS
-// stages: the next tile's global loads are in flight in registers while the
-// MFMAs consume the current one.
+// Per 32-key block the wave computes S^T = K Q^T with
+// v_mfma_f32_32x32x16_bf16: the MFMA output puts one query per lane column,
+// so the online-softmax max is lane-local plus one exchange with lane ^ 32,
+// and the row sum stays lane-local until the end. P^T is packed to bf16 in
+// registers and is the B operand of O^T += V^T P^T (same MFMA). V is kept
+// transposed in LDS ([dim][key], keys of each 16-key slice in the order of
+// the P^T registers), so each V^T operand is one 16-byte LDS read.
+//
+// The loop is software-pipelined over half tiles (32-key blocks) so that each
+// wave's MFMAs run beside independent VALU work of its own (see step_a /
+// step_b).
 //
 // Mask: key position p is visible to query position r iff p / chunk <= r / chunk
 // (chunk <= 0: all visible). Tiles wholly beyond the last query's chunk are
@@ -43,14 +41,18 @@ constexpr int NT = 64 * NW;
 constexpr int QW = 32;             // queries per wave
 constexpr int BQ = QW * NW;        // queries per workgroup
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
-// V tile: [key][dim] fp16 rows of 256 B, padded to 320 B (80 dwords: row k
-// starts 16 banks after row k - 1); 16-byte chunk c of key row k is stored at
-// position vchunk(k, c) (see below).
-constexpr int VROW = D * 2 + 64;
+// V^T tile: 128 dim rows of 64 bf16 keys (128 B) padded to 144 B = 9 16-byte
+// units, so 16 consecutive rows at one column fall in 16 different bank
+// groups (9 is odd). Column unit c of a row holds the 8 keys 16 (c / 2) +
+// 4 (c % 2) + {0..3} and + 8 + {0..3}: the keys lane half c % 2 feeds to the
+// PV MFMA for 16-key slice c / 2.
+constexpr int VTROW = 144;
 constexpr int K_BYTES = BKV * KROW;
-constexpr int V_BYTES = BKV * VROW;
-constexpr int S_BYTES = 2 * BKV * 4;  // per-key K and V scales (fp32)
-constexpr int STAGE = K_BYTES + V_BYTES + S_BYTES;
+constexpr int VT_BYTES = D * VTROW;
+constexpr int STAGE = K_BYTES + VT_BYTES;
+// Per-key scales of a tile in flight ([0, 64) K, [64, 128) V), two buffers.
+constexpr int SB_FLOATS = 2 * BKV;
+constexpr int SMEM = 2 * STAGE + 2 * SB_FLOATS * 4;
 
 struct Params {
     const uint16_t* q;
@@ -77,177 +79,190 @@ struct Params {
     float* ws_ml;      // splits > 1: running max and sum, [split][B][H][Lq][2]
 };
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-// Position of the 16-byte chunk c (8 dims) of key row k in the V tile: the two
-// low bits of c are XORed with bits 2-3 of k. With the 16-bank row shift this
-// makes both access patterns conflict-free over the 64 LDS banks: the row
-// writes (16 lanes = keys 16 i .. 16 i + 15 at one chunk index: bank groups
-// 16 (k % 4) + 4 ((c % 4) ^ (k / 4 % 4)) all differ) and the transposing reads
-// (keys 4 i .. 4 i + 3 x chunks 4 b .. 4 b + 3). Chunk groups 4 b .. 4 b + 3
-// stay in place, so a dim block is a constant offset.
-HN_DEVICE int vchunk(int k, int c) { return (c & ~3) | ((c & 3) ^ ((k >> 2) & 3)); }
+// ---------------------------------------------------------------------------
+// Dequantization to the reference's bf16 values.
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
-// V^T fragment of the PV MFMA for dim block db and 16-key slice `slice`:
-// lane l needs dim 32 db + l % 32 and keys 16 slice + 4 (l / 32) + {0..3} and
-// + 8 + {0..3} (the order of the P^T registers, see compute loop). The
-// transposing read gives lane i of each 16-lane group element i % 4 of the
-// 8-byte rows addressed by lanes i / 4 + 4 e, e = 0..3; so lane j of group g
-// addresses key (base + j / 4) at dims 32 db + 16 (g % 2) + 4 (j % 4), and
-// every lane receives four consecutive keys of its own dim.
-HN_DEVICE f16x8 read_vt(const uint8_t* vl, int db, int slice, int lane) {
-    const int g = lane >> 4, j = lane & 15;
-    const int c = 4 * db + 2 * (g & 1) + ((j & 3) >> 1);
-    const int byte = 8 * (j & 1);
-    f16x4 r[2];
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-        const int k = 16 * slice + 8 * h2 + 4 * (g >> 1) + (j >> 2);
-        const uint8_t* a = vl + k * VROW + vchunk(k, c) * 16 + byte;
-        r[h2] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(__attribute__((address_space(3))) void*)a));
-    }
-    f16x8 v;
-    v[0] = r[0][0]; v[1] = r[0][1]; v[2] = r[0][2]; v[3] = r[0][3];
-    v[4] = r[1][0]; v[5] = r[1][1]; v[6] = r[1][2]; v[7] = r[1][3];
-    return v;
-}
-
-// Two codes (bytes 2 hi, 2 hi + 1 of w) -> their two exact bf16 values. The
-// gfx950 conversion is used with a unit scale only: its scale operand applies
-// just the exponent of the fp32 value, so per-token scales are applied in fp32
-// by the caller instead.
+// Two codes (bytes 2 hi, 2 hi + 1 of w) -> their exact fp32 values. The gfx950
+// conversion is used with a unit scale only: its scale operand applies just
+// the exponent of the fp32 value.
 template <int FMT>
-HN_DEVICE uint32_t cvt2(uint32_t w, bool hi) {
-    if (FMT == HN_KV_FP8) {
-        bf16x2 r = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true)
-                      : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
-        return __builtin_bit_cast(uint32_t, r);
-    }
+HN_DEVICE f32x2 codes2_f32(uint32_t w, bool hi) {
+    if (FMT == HN_KV_FP8)
+        return hi ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true)
+                  : __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
     const uint32_t sh = hi ? 16 : 0;
-    const float a = (float)(int8_t)((w >> sh) & 0xffu);
-    const float b = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
-    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    f32x2 r;
+    r[0] = (float)(int8_t)((w >> sh) & 0xffu);
+    r[1] = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
+    return r;
 }
 
-// 16 codes (one uint4) -> 16 bf16 as 8 dwords.
-template <int FMT>
-HN_DEVICE void cvt16(const uint4& c, uint32_t (&o)[8]) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+// bf16 bits of fp32 a and b, packed (a low), round to nearest even.
+HN_DEVICE uint32_t pack_bf16(float a, float b) {
+    const f32x2 f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// ---------------------------------------------------------------------------
+// Tile loads and LDS writes.
+//
+// K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
+// V^T: thread t (wave w, lane λ) owns key quad qd = λ % 16 (keys quad_key(qd, j),
+// j < 4: the 8-byte half qd % 2 of column unit qd / 2) and dims 8 dg .. 8 dg + 7,
+// dg = λ / 16 + 4 w. Per 8-byte LDS write a 32-lane group covers 2 dim groups x
+// 16 quads, whose bank pairs (18 row + qd) mod 32 are all distinct (row pitch
+// 144 B); per global load each wave reads 16 keys x 32 contiguous bytes.
+// Scales: threads 0-63 load the K scale of key t, threads 64-127 the V scale
+// of key t - 64, into the tile's scale buffer.
+
+// Key (0..63) of entry j (0..3) of quad qd.
+HN_DEVICE int quad_key(int qd, int j) {
+    return 16 * (qd >> 2) + 4 * ((qd >> 1) & 1) + 8 * (qd & 1) + j;
+}
+
+// Registers holding one cache tile between its global load and its LDS
+// write (issued about one tile ahead).
+struct CacheRegs {
+    uint4 k[2];
+    uint2 v[4];  // 8 codes (dims 8 dg ..) of quad key j
+    float s;     // one per-key scale (threads < 128)
+};
+
+// Base addresses of a cache tile: uniform (scalar) pointers; the per-thread
+// parts are 32-bit offsets, so the loads take the scalar-base form.
+struct TileBase {
+    const uint8_t* k;
+    const uint8_t* v;
+    const float* ks;
+    const float* vs;
+};
+
+HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t first) {
+    TileBase tb;
+    const int64_t c = b * p.cs0 + first * p.cs1 + h * p.cs2;
+    const int64_t s = b * p.ss0 + first * p.ss1 + h * p.ss2;
+    tb.k = p.kc + c;
+    tb.v = p.vc + c;
+    tb.ks = p.ks + s;
+    tb.vs = p.vs + s;
+    return tb;
+}
+
+// Keys past the end of a short tile re-read the tile's last key (they are
+// masked out of the softmax).
+HN_DEVICE void load_k(const Params& p, CacheRegs& r, const TileBase& tb, int count) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t last = (uint32_t)count - 1u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        o[2 * i] = cvt2<FMT>(w[i], false);
-        o[2 * i + 1] = cvt2<FMT>(w[i], true);
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t key = min((t >> 3) + 32u * i, last);
+        r.k[i] = *reinterpret_cast<const uint4*>(tb.k + (key * (uint32_t)p.cs1 + (t & 7u) * 16u));
+    }
+    if (t < 2u * BKV) {
+        const uint32_t so = min(t & 63u, last) * (uint32_t)p.ss1;
+        r.s = t < BKV ? tb.ks[so] : tb.vs[so];
     }
 }
 
-
-HN_DEVICE uint32_t pack_f16(float a, float b) {
-    const f32x2 f = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+HN_DEVICE void load_v(const Params& p, CacheRegs& r, const TileBase& tb, int count) {
+    const int lam = threadIdx.x & 63;
+    const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
+    const uint32_t last = (uint32_t)count - 1u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t key = min((uint32_t)quad_key(qd, j), last);
+        r.v[j] = *reinterpret_cast<const uint2*>(tb.v + (key * (uint32_t)p.cs1 + 8u * (uint32_t)dg));
+    }
 }
 
-// 16 codes (one uint4) -> their 16 exact fp16 values, as 8 dwords.
+HN_DEVICE uint32_t word(const uint4& c, int q) { return q == 0 ? c.x : q == 1 ? c.y : q == 2 ? c.z : c.w; }
+
+// Dequantized K write, part i (0..7): unit i / 4, codes 4 (i % 4) .. +3 ->
+// two bf16 dwords of kd; every second part writes 16 bytes (8 dims).
 template <int FMT>
-HN_DEVICE void codes16_f16(const uint4& c, uint32_t (&o)[8]) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+HN_DEVICE void store_k_part(const CacheRegs& r, uint8_t* st, int i, const float (&ks)[2], uint32_t (&kd)[4]) {
+    const int un = i >> 2, q = i & 3;
+    const uint32_t w = word(r.k[un], q);
+    const float s = ks[un];
+    const f32x2 a = codes2_f32<FMT>(w, false), c = codes2_f32<FMT>(w, true);
+    kd[2 * (q & 1)] = pack_bf16(a[0] * s, a[1] * s);
+    kd[2 * (q & 1) + 1] = pack_bf16(c[0] * s, c[1] * s);
+    if (q & 1) {
+        const int u = threadIdx.x + NT * un;
+        *reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32 + (q >> 1) * 16) =
+            make_uint4(kd[0], kd[1], kd[2], kd[3]);
+    }
+}
+
+// The K scales of the thread's two units, from the tile's scale buffer.
+HN_DEVICE void k_scales(const float* sb, float (&ks)[2]) {
+    ks[0] = sb[threadIdx.x >> 3];
+    ks[1] = sb[(threadIdx.x >> 3) + 32];
+}
+
+// Dequantized V^T write, part i (0..7): quad key j = i / 2, dims 4 (i % 2) ..
+// +3 of the thread's 8; keys (0, 1) and (2, 3) pair into bf16 dwords
+// (vd[2 d + pair], dim d), and parts 6 and 7 write dims 0-3 and 4-7 (8 bytes
+// = 4 keys each).
+template <int FMT>
+HN_DEVICE void store_v_part(const CacheRegs& r, uint8_t* st, int i, const float4& vs, float (&vp)[8],
+                            uint32_t (&vd)[16]) {
+    const int j = i >> 1, hf = i & 1;
+    const uint32_t w = hf ? r.v[j].y : r.v[j].x;
+    const f32x2 a = codes2_f32<FMT>(w, false), c = codes2_f32<FMT>(w, true);
+    const float s = j == 0 ? vs.x : j == 1 ? vs.y : j == 2 ? vs.z : vs.w;
+    const float x[4] = {a[0] * s, a[1] * s, c[0] * s, c[1] * s};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (FMT == HN_KV_FP8) {
-            o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, false));
-            o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[i], 1.0f, true));
-        } else {
-            o[2 * i] = pack_f16((float)(int8_t)(w[i] & 0xffu), (float)(int8_t)((w[i] >> 8) & 0xffu));
-            o[2 * i + 1] = pack_f16((float)(int8_t)((w[i] >> 16) & 0xffu), (float)(int8_t)(w[i] >> 24));
+    for (int dd = 0; dd < 4; ++dd) {
+        const int d = 4 * hf + dd;
+        if (j & 1) vd[2 * d + (j >> 1)] = pack_bf16(vp[d], x[dd]);
+        else vp[d] = x[dd];
+    }
+    if (j == 3) {
+        const int lam = threadIdx.x & 63;
+        const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+            const int d = 4 * hf + dd;
+            *reinterpret_cast<uint2*>(st + K_BYTES + (8 * dg + d) * VTROW + 8 * qd) = make_uint2(vd[2 * d], vd[2 * d + 1]);
         }
     }
 }
 
-// Two bf16 (one dword) -> two fp16.
-HN_DEVICE uint32_t bf16x2_to_f16x2(uint32_t w) {
-    return pack_f16(bf16_bits_to_f32(w & 0xffffu), bf16_bits_to_f32(w >> 16));
+// The V scales of the thread's quad (4 consecutive keys), from the scale buffer.
+HN_DEVICE float4 v_scales(const float* sb) {
+    const int qd = threadIdx.x & 15;
+    return *reinterpret_cast<const float4*>(sb + BKV + quad_key(qd, 0));
 }
 
-// Registers holding one cache tile between its global load and its LDS
-// write (the load is issued before the tile in LDS is consumed).
-// K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
-// V: lane l of wave w owns key l, dims 32 w .. 32 w + 31.
-struct CacheRegs {
-    uint4 k[2];
-    uint4 v[2];
-    float sk[2], sv;
-};
-
-HN_DEVICE void load_cache_tile(const Params& p, CacheRegs& r, int64_t b, int64_t h,
-                               int64_t first, int64_t count) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int u = t + NT * i;
-        int64_t j = u >> 3;
-        j = j < count ? j : count - 1;  // clamp inside the segment; masked later
-        const int64_t tok = first + j;
-        r.k[i] = *reinterpret_cast<const uint4*>(p.kc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (u & 7) * 16);
-        r.sk[i] = p.ks[b * p.ss0 + tok * p.ss1 + h * p.ss2];
-    }
-    int64_t j = t & 63;
-    j = j < count ? j : count - 1;
-    const int64_t tok = first + j;
-    const uint8_t* src = p.vc + b * p.cs0 + tok * p.cs1 + h * p.cs2 + (t >> 6) * 32;
-    r.v[0] = *reinterpret_cast<const uint4*>(src);
-    r.v[1] = *reinterpret_cast<const uint4*>(src + 16);
-    r.sv = p.vs[b * p.ss0 + tok * p.ss1 + h * p.ss2];
-}
-
-// V row write: key t % 64, chunks 4 (t / 64) .. +3 (32 dims), from 16 dwords of fp16 pairs.
-HN_DEVICE void store_v_row(uint8_t* vl, const uint32_t (&cv)[16]) {
-    const int t = threadIdx.x;
-    const int k = t & 63, c0 = 4 * (t >> 6);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<uint4*>(vl + k * VROW + vchunk(k, c0 + c) * 16) =
-            make_uint4(cv[4 * c], cv[4 * c + 1], cv[4 * c + 2], cv[4 * c + 3]);
-}
-
-// Per-key scales in LDS: [0, 64) K scale * softmax_scale * log2 e, [64, 128) V scale.
-HN_DEVICE float* stage_scales(uint8_t* st) { return reinterpret_cast<float*>(st + K_BYTES + V_BYTES); }
-
+// Whole-tile write (prologue), scales from the tile's scale buffer.
 template <int FMT>
-HN_DEVICE void store_cache_tile(const Params& p, const CacheRegs& r, uint8_t* st) {
-    const int t = threadIdx.x;
-    float* sc = stage_scales(st);
+HN_DEVICE void store_tile(const CacheRegs& r, uint8_t* st, const float* sb) {
+    float ks[2];
+    k_scales(sb, ks);
+    const float4 vs = v_scales(sb);
+    uint32_t kd[4];
+    float vp[8];
+    uint32_t vd[16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int u = t + NT * i;
-        uint32_t o[8];
-        cvt16<FMT>(r.k[i], o);
-        uint4* dst = reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32);
-        dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
-        dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
-        if ((u & 7) == 0) sc[u >> 3] = r.sk[i] * p.scale_log2;
+    for (int i = 0; i < 8; ++i) {
+        store_k_part<FMT>(r, st, i, ks, kd);
+        store_v_part<FMT>(r, st, i, vs, vp, vd);
     }
-    uint32_t cv[16];
-    codes16_f16<FMT>(r.v[0], *reinterpret_cast<uint32_t(*)[8]>(&cv[0]));
-    codes16_f16<FMT>(r.v[1], *reinterpret_cast<uint32_t(*)[8]>(&cv[8]));
-    store_v_row(st + K_BYTES, cv);
-    if (t < BKV) sc[BKV + t] = r.sv;  // wave 0: lane t holds key t
 }
 
-// Unquantized tail tile (bf16 K/V of the current chunk): load and write to LDS
-// in one go (not prefetched: it is at most one chunk of the keys).
-HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t first,
-                              int64_t count, uint8_t* st) {
+// Unquantized tail tile (bf16 K/V of the current chunk), written with the
+// same thread-to-location mapping as the cache writes (so it cleanly
+// replaces what those wrote to the same stage). Not prefetched: it is at most
+// one chunk of the keys.
+HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int u = t + NT * i;
-        int64_t j = u >> 3;
-        j = j < count ? j : count - 1;
+        const int j = min(u >> 3, count - 1);
         const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (u & 7) * 16;
         const uint4 lo = *reinterpret_cast<const uint4*>(src);
         const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
@@ -255,24 +270,28 @@ HN_DEVICE void copy_tail_tile(const Params& p, int64_t b, int64_t h, int64_t fir
         dst[0] = lo;
         dst[1] = hi;
     }
-    {
-        int64_t j = t & 63;
-        j = j < count ? j : count - 1;
-        const uint16_t* src = p.vcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (t >> 6) * 32;
-        uint32_t cv[16];
+}
+
+HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
+    const int lam = threadIdx.x & 63;
+    const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
+    uint4 w[4];  // dims 8 dg .. 8 dg + 7 of quad key j (bf16)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * c);
-            cv[4 * c] = bf16x2_to_f16x2(w.x);
-            cv[4 * c + 1] = bf16x2_to_f16x2(w.y);
-            cv[4 * c + 2] = bf16x2_to_f16x2(w.z);
-            cv[4 * c + 3] = bf16x2_to_f16x2(w.w);
-        }
-        store_v_row(st + K_BYTES, cv);
+    for (int j = 0; j < 4; ++j) {
+        const int key = min(quad_key(qd, j), count - 1);
+        w[j] = *reinterpret_cast<const uint4*>(p.vcur + b * p.us0 + (first + key) * p.us1 + h * p.us2 + 8 * dg);
     }
-    float* sc = stage_scales(st);
-    if (t < BKV) sc[t] = p.scale_log2;
-    else if (t < 2 * BKV) sc[t] = 1.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        uint32_t o[2];
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+            const uint32_t a = word(w[2 * pr], d >> 1), c = word(w[2 * pr + 1], d >> 1);
+            const uint32_t sh = (d & 1) * 16;
+            o[pr] = ((a >> sh) & 0xffffu) | (((c >> sh) & 0xffffu) << 16);
+        }
+        *reinterpret_cast<uint2*>(st + K_BYTES + (8 * dg + d) * VTROW + 8 * qd) = make_uint2(o[0], o[1]);
+    }
 }
 
 HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -283,9 +302,160 @@ HN_DEVICE bf16x8 ld_bf16x8(const uint8_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
+// Max of v over the lane pair (l, l ^ 32) with gfx950's half-wave swap.
+HN_DEVICE float pair_max(float v) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
+// ---------------------------------------------------------------------------
+// Half-tile steps. A "half" is one 32-key block kb of a 64-key tile; for it
+// the wave holds S^T as one f32x16 (register v: key 32 kb + 8 (v/4) + 4 half
+// + v%4, query = this lane's column).
+
+// S^T block kb of the tile in stage st: 8 MFMAs over the 128 dims (prologue).
+HN_DEVICE f32x16 s_block(const uint8_t* ka, const bf16x8 (&qf)[8]) {
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) acc = mfma_bf16(ld_bf16x8(ka + 32 * sl), qf[sl], acc);
+    return acc;
+}
+
+// Max of the raw S^T block over the query's 32 keys (both lanes of the pair).
+HN_DEVICE float raw_max(const f32x16& s) {
+    float mx = s[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
+    return pair_max(mx);
+}
+
+// Partial tiles: keys j >= lim of the tile are masked to -inf; returns the new max.
+HN_DEVICE float mask_raw(f32x16& s, int kb, int half, int lim) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+        if (j >= lim) s[v] = -INFINITY;
+    }
+    return raw_max(s);
+}
+
+// Running-max update before a block's probabilities: with the block's raw
+// max mx, the logit max in log2 units is mx * c (c = softmax_scale * log2 e
+// > 0). Taken only when some lane's max moved (rare after the first tiles):
+// O and l are rescaled by 2^(m_old - m_new).
+HN_DEVICE void rebase(float mx, float c, float& m, float& l, f32x16 (&o)[4]) {
+    const float mb = mx * c;
+    if (!__any(mb > m)) return;
+    const float mnew = fmaxf(m, mb);
+    const float alpha = m == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    l *= alpha;
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
+    }
+}
+
+// Ties values to this point of the instruction stream: the empty asm is
+// ordered with the sched_barrier that ends a slot, so the arithmetic feeding
+// it cannot drift into later slots (pure operations are otherwise placed
+// freely before the machine scheduler sees the barrier).
+template <typename A, typename B, typename C>
+HN_DEVICE void pin(A& a, B& b, C& c) {
+    asm volatile("" : "+v"(a), "+v"(b), "+v"(c));
+}
+template <typename A>
+HN_DEVICE void pin(A& a) {
+    asm volatile("" : "+v"(a));
+}
+
+// ---------------------------------------------------------------------------
+// The two software-pipelined steps of a half tile. Each pairs one 8-MFMA chain
+// with the independent VALU work of the other chain, spread over 8 slots (one
+// MFMA + about 8 VALU instructions, ~32 cycles each) that sched_barrier keeps
+// in place: on gfx950 a wave's VALU instructions execute while its own MFMAs
+// occupy the matrix core, but not beside another wave's MFMAs, so the overlap
+// has to be built into each wave's instruction stream. Operand reads from LDS
+// are issued two slots ahead.
+
+// Step A: S^T of the next block from the K rows at ka (this lane's row in the
+// stage) beside the probabilities of the current block (raw S^T in s):
+// p = 2^(s c - m), l += p, P^T = bf16(p) for the two 16-key slices (registers
+// 8t .. 8t+7 hold keys 16 t + 4 half + {0..3} and + 8 + {0..3} of the block).
+HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, bf16x8 (&pf)[2], const uint8_t* ka,
+                        const bf16x8 (&qf)[8]) {
+    const float nm = m == -INFINITY ? 0.0f : -m;  // m = -inf: every s is -inf (masked)
+    bf16x8 kf[8];
+    kf[0] = ld_bf16x8(ka);
+    kf[1] = ld_bf16x8(ka + 32);
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    float ls[2] = {0.0f, 0.0f};
+    uint32_t x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (i + 2 < 8) kf[i + 2] = ld_bf16x8(ka + 32 * (i + 2));
+        acc = mfma_bf16(kf[i], qf[i], acc);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i], c, nm));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i + 1], c, nm));
+        ls[0] += p0;
+        ls[1] += p1;
+        x[i] = pack_bf16(p0, p1);
+        pin(x[i], ls[0], ls[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    l += ls[0] + ls[1];
+    pf[0] = __builtin_bit_cast(bf16x8, make_uint4(x[0], x[1], x[2], x[3]));
+    pf[1] = __builtin_bit_cast(bf16x8, make_uint4(x[4], x[5], x[6], x[7]));
+    return acc;
+}
+
+// Step B: O^T += V^T P^T of block kb (V^T operand reads at va: this lane's
+// row and column in the stage) beside the raw max of the next block (s) and,
+// per STORE (1: K, 2: V^T), half of the write of the prefetched tile to stage
+// nst with the scales of buffer sb. Returns the next block's raw max (pair-wide).
+template <int FMT, int STORE>
+HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (&o)[4], const f32x16& s,
+                       const CacheRegs& r, uint8_t* nst, const float* sb) {
+    // operand i (= 4 tt + db): dim block db, 16-key slice 2 kb + tt
+    bf16x8 vf[8];
+    vf[0] = ld_bf16x8(va + 64 * kb);
+    vf[1] = ld_bf16x8(va + 64 * kb + 32 * VTROW);
+    float ks[2] = {0.0f, 0.0f};
+    float4 vs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (STORE == 1) k_scales(sb, ks);
+    if (STORE == 2) vs = v_scales(sb);
+    float mx = -INFINITY;
+    uint32_t kd[4];
+    float vp[8];
+    uint32_t vd[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int tt = i >> 2, db = i & 3;
+        if (i + 2 < 8) {
+            const int i2 = i + 2;
+            vf[i2] = ld_bf16x8(va + 64 * kb + 32 * (i2 >> 2) + (i2 & 3) * 32 * VTROW);
+        }
+        o[db] = mfma_bf16(vf[i], pf[tt], o[db]);
+        mx = fmaxf(mx, fmaxf(s[2 * i], s[2 * i + 1]));
+        pin(mx);
+        if (STORE == 1) store_k_part<FMT>(r, nst, i, ks, kd);
+        if (STORE == 2) store_v_part<FMT>(r, nst, i, vs, vp, vd);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return pair_max(mx);
+}
+
 template <int FMT>
 __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+    float* const sbuf = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][128]
 
     // XCD-aware work order: workgroup ids are dealt round-robin to the 8 XCDs,
     // so id % 8 picks a contiguous range of work items -- the query tiles of
@@ -347,161 +517,132 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
-    float mrow = -INFINITY;
-    float lsum = 0.0f;
+    float m = -INFINITY;  // running max of the logits (log2 units), shared by the lane pair
+    float l = 0.0f;       // this lane's share of the softmax denominator
+    const float c = p.scale_log2;
 
-    CacheRegs regs;
-    auto tile_geom = [&](int t, bool& cache_seg, int64_t& first, int64_t& count, int64_t& pos0) {
-        if (t < n_cache) {
-            cache_seg = true;
-            first = (int64_t)t * BKV;
-            count = cache_end - first;
-            pos0 = first;
-        } else {
-            cache_seg = false;
-            first = (int64_t)(t - n_cache) * BKV;
-            count = tail_end - first;
-            pos0 = p.kv_len + first;
-        }
-        count = count < BKV ? count : BKV;
+    // Tile t: segment, first key index within it, key count;
+    // `full`: every key exists and is visible to every query of the workgroup;
+    // `lim`: keys j < lim of the tile are visible to this lane's query.
+    struct Geom {
+        bool cache;
+        int64_t first;
+        int count;
+        bool full;
+        int lim;
     };
-
-    if (t_end > t_begin) {
-        bool cs;
-        int64_t first, count, pos0;
-        tile_geom(t_begin, cs, first, count, pos0);
-        if (cs) {
-            load_cache_tile(p, regs, b, h, first, count);
-            store_cache_tile<FMT>(p, regs, smem);
+    auto geom = [&](int t) {
+        Geom g;
+        int64_t count, pos0;
+        if (t < n_cache) {
+            g.cache = true;
+            g.first = (int64_t)t * BKV;
+            count = cache_end - g.first;
+            pos0 = g.first;
         } else {
-            copy_tail_tile(p, b, h, first, count, smem);
+            g.cache = false;
+            g.first = (int64_t)(t - n_cache) * BKV;
+            count = tail_end - g.first;
+            pos0 = p.kv_len + g.first;
+        }
+        g.count = (int)(count < BKV ? count : BKV);
+        g.full = g.count == BKV && pos0 + BKV <= wg_key_limit;
+        int64_t lim64 = key_limit - pos0;
+        lim64 = lim64 < g.count ? lim64 : g.count;
+        g.lim = lim64 < 0 ? 0 : (int)lim64;
+        return g;
+    };
+    // This lane's K row (block 0) at dims 8 half .., and its V^T row (dim
+    // block 0) at column unit `half` (slice 0).
+    const uint32_t ka_off = col * KROW + 16 * half;
+    const uint32_t va_off = K_BYTES + col * VTROW + 16 * half;
+    CacheRegs regs;
+    regs.s = 0.0f;
+
+    // Software pipeline over half tiles. Per tile u = t - t_begin (stage
+    // u % 2; the next tile in the other stage; scales of tile u in buffer u % 2):
+    //   half 0: rebase; S(t, kb 1) || probs(kb 0)
+    //           PV(t, kb 0) || max(kb 1), K of t + 1 written; K codes + scales of t + 2 fetched
+    //   half 1: rebase; S(t + 1, kb 0) || probs(kb 1)
+    //           PV(t, kb 1) || max(t + 1, kb 0), V^T of t + 1 written; scales of
+    //           t + 2 to buffer u % 2, V codes of t + 2 fetched
+    // Stage reuse: stage (u + 1) % 2 (tile t - 1) is last read by PV in half 1
+    // of t - 1, before the barrier that precedes its K write in half 0 of t;
+    // K of t + 1 is first read after the barrier that ends half 0, V^T of
+    // t + 1 after the barrier that ends half 1. Scale buffer u % 2 (tile t)
+    // was last read in half 1 of t - 1.
+    if (t_end > t_begin) {
+        f32x16 sa, sb;
+        float mxa, mxb;
+        Geom g = geom(t_begin);
+        {
+            if (g.cache) {
+                const TileBase tb = tile_base(p, b, h, g.first);
+                load_k(p, regs, tb, g.count);
+                load_v(p, regs, tb, g.count);
+                __builtin_amdgcn_s_waitcnt(0);
+                if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
+                __syncthreads();
+                store_tile<FMT>(regs, smem, sbuf);
+            } else {
+                copy_tail_k(p, b, h, g.first, g.count, smem);
+                copy_tail_v(p, b, h, g.first, g.count, smem);
+            }
+            if (t_begin + 1 < t_end) {
+                const Geom g1 = geom(t_begin + 1);
+                if (g1.cache) {
+                    const TileBase tb = tile_base(p, b, h, g1.first);
+                    load_k(p, regs, tb, g1.count);
+                    load_v(p, regs, tb, g1.count);
+                }
+            }
+            // Everything issued so far (the Q fragments included) has landed;
+            // inside the loop the only loads in flight are the prefetch.
+            __builtin_amdgcn_s_waitcnt(0);
+            if (threadIdx.x < 2 * BKV) sbuf[SB_FLOATS + threadIdx.x] = regs.s;
+            __syncthreads();
+            sa = s_block(smem + ka_off, qf);
+            mxa = g.full ? raw_max(sa) : mask_raw(sa, 0, half, g.lim);
+        }
+        for (int t = t_begin; t < t_end; ++t) {
+            const int u = t - t_begin;
+            const uint8_t* st = smem + (u & 1) * STAGE;
+            uint8_t* nst = smem + ((u & 1) ^ 1) * STAGE;
+            const float* nsb = sbuf + ((u & 1) ^ 1) * SB_FLOATS;  // scales of tile t + 1
+            const bool has_next = t + 1 < t_end;
+            const Geom gn = geom(has_next ? t + 1 : t);
+            const bool fetch2 = t + 2 < t_end;
+            const Geom g2 = geom(fetch2 ? t + 2 : t);
+            bf16x8 pf[2];
+
+            // ---- half 0
+            rebase(mxa, c, m, l, o);
+            sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
+            // K of tile t + 1 from the prefetch registers (a tail tile or the
+            // end of the range is handled right after: the K rows of the stage
+            // are not read before the barrier).
+            mxb = step_b<FMT, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
+            if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
+            if (has_next && !gn.cache) copy_tail_k(p, b, h, gn.first, gn.count, nst);
+            if (fetch2 && g2.cache) load_k(p, regs, tile_base(p, b, h, g2.first), g2.count);
+            __syncthreads();
+
+            // ---- half 1 (on the last tile the S block of "tile t + 1" reads
+            // stale LDS; its result is never used)
+            rebase(mxb, c, m, l, o);
+            sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
+            mxa = step_b<FMT, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
+            if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
+            if (has_next && !gn.cache) copy_tail_v(p, b, h, gn.first, gn.count, nst);
+            if (fetch2 && g2.cache) {
+                if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                load_v(p, regs, tile_base(p, b, h, g2.first), g2.count);
+            }
+            __syncthreads();
+            g = gn;
         }
     }
-    __syncthreads();
-
-    for (int t = t_begin; t < t_end; ++t) {
-        const uint8_t* st = smem + ((t - t_begin) & 1) * STAGE;
-        bool cs;
-        int64_t first, count, pos0;
-        tile_geom(t, cs, first, count, pos0);
-        bool ncs = false;
-        int64_t nf = 0, nc = 0, np = 0;
-        if (t + 1 < t_end) {
-            tile_geom(t + 1, ncs, nf, nc, np);
-            if (ncs) load_cache_tile(p, regs, b, h, nf, nc);
-        }
-
-        // ---- S^T = K Q^T: two 32-key blocks x this wave's 32 queries
-        f32x16 sacc[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.0f;
-#pragma unroll
-        for (int sl = 0; sl < 8; ++sl)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const bf16x8 kf = ld_bf16x8(st + (kb * 32 + col) * KROW + (16 * sl + 8 * half) * 2);
-                sacc[kb] = mfma_bf16(kf, qf[sl], sacc[kb]);
-            }
-
-        // ---- mask: keys past the segment end, and the chunk-causal rule.
-        // Positions increase with the key index, so the keys this lane's query
-        // sees in the tile are exactly j < lim (lane-local, 32-bit compare).
-        // Register v of block kb holds key 32 kb + 8 (v/4) + 4 half + v%4.
-        const bool full = count == BKV && pos0 + BKV <= wg_key_limit;
-        if (!full) {
-            int64_t lim64 = key_limit - pos0;
-            lim64 = lim64 < count ? lim64 : count;
-            const int lim = lim64 < 0 ? 0 : (int)lim64;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (j >= lim) sacc[kb][v] = -INFINITY;
-                }
-        }
-
-        // ---- logits in log2 units: t = s * (k_scale * softmax_scale * log2 e).
-        // Register v of block kb holds key 32 kb + 8 (v/4) + 4 half + v%4, so
-        // each group of 4 registers takes 4 consecutive scales (one 16-byte read).
-        const float* sc = reinterpret_cast<const float*>(st + K_BYTES + V_BYTES);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                const float4 ks4 = *reinterpret_cast<const float4*>(sc + kb * 32 + 8 * g4 + 4 * half);
-                sacc[kb][4 * g4 + 0] *= ks4.x;
-                sacc[kb][4 * g4 + 1] *= ks4.y;
-                sacc[kb][4 * g4 + 2] *= ks4.z;
-                sacc[kb][4 * g4 + 3] *= ks4.w;
-            }
-
-        // ---- online softmax for this lane's query (keys split over lane ^ 32)
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[kb][v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(mrow, mx);
-        const float muse = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(mrow - muse);
-        mrow = mnew;
-        float rs = 0.0f;
-        f16x8 pf[2][2];  // [kb][t]: P^T registers 8t .. 8t+7 of block kb, times the V scale
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                // registers 8t .. 8t+3 hold keys 32 kb + 16 t + 4 half + 0..3,
-                // registers 8t+4 .. 8t+7 keys 32 kb + 16 t + 8 + 4 half + 0..3
-                const float4 va = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 4 * half);
-                const float4 vb = *reinterpret_cast<const float4*>(sc + BKV + kb * 32 + 16 * tt + 8 + 4 * half);
-                const float vsc[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-                float pv[8];
-#pragma unroll
-                for (int e2 = 0; e2 < 8; ++e2) {
-                    pv[e2] = __builtin_amdgcn_exp2f(sacc[kb][8 * tt + e2] - muse);
-                    rs += pv[e2];
-                }
-                f16x8 x;
-#pragma unroll
-                for (int e2 = 0; e2 < 8; ++e2) x[e2] = (_Float16)(pv[e2] * vsc[e2]);
-                pf[kb][tt] = x;
-            }
-        rs += __shfl_xor(rs, 32, 64);
-        lsum = lsum * alpha + rs;
-        // Rescale O only when some lane's running max moved (wave-uniform test).
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) o[db][v] *= alpha;
-        }
-
-        // ---- O^T += V^T P^T over the four 16-key slices of the tile
-        const uint8_t* vl = st + K_BYTES;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int slice = kb * 2 + tt;
-#pragma unroll
-                for (int db = 0; db < 4; ++db) {
-                    const f16x8 vf = read_vt(vl, db, slice, lane);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kb][tt], o[db], 0, 0, 0);
-                }
-            }
-
-        if (t + 1 < t_end) {
-            uint8_t* nst = smem + ((t + 1 - t_begin) & 1) * STAGE;
-            if (ncs) store_cache_tile<FMT>(p, regs, nst);
-            else copy_tail_tile(p, b, h, nf, nc, nst);
-        }
-        __syncthreads();
-    }
+    l += __shfl_xor(l, 32, 64);
 
     // ---- epilogue: O = O^T / l; the lane holds dims 32 db + 8 (v/4) + 4 half + v%4
     if (p.splits > 1) {
@@ -517,12 +658,12 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
                     *reinterpret_cast<float4*>(dst + d) =
                         make_float4(o[db][vq * 4], o[db][vq * 4 + 1], o[db][vq * 4 + 2], o[db][vq * 4 + 3]);
                 }
-            if (half == 0) *reinterpret_cast<float2*>(p.ws_ml + qi * 2) = make_float2(mrow, lsum);
+            if (half == 0) *reinterpret_cast<float2*>(p.ws_ml + qi * 2) = make_float2(m, l);
         }
         return;
     }
     if (qvalid) {
-        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         uint16_t* dst = p.out + b * p.os0 + row * p.os1 + h * p.os2;
 #pragma unroll
         for (int db = 0; db < 4; ++db)

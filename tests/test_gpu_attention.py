@@ -1,6 +1,12 @@
 """GPU parity of the FP8-KV chunk attention against the oracle's float64
-softmax(Q K^T / sqrt(D)) V with K, V = code * scale read from the same cache.
-Bar: max-abs 2e-2 and rel-L2 1e-2."""
+softmax(Q K^T / sqrt(D)) V over the K, V the reference attends over: the
+cache decoded to bf16(code * scale). Bar: max-abs 2e-2 and rel-L2 1e-2.
+
+Like the reference's flash attention, the kernel multiplies probabilities
+rounded to bf16 into V (|bf16(p) - p| <= 2^-8 p), so an output element may
+differ from the exact-softmax oracle by up to 2^-8 * sum_k p_k |v_k| / l. The
+elementwise bound adds that term, computed by the oracle from the same softmax
+weights applied to |V| (P_ROUND * envelope); the rel-L2 bar is unchanged."""
 import numpy as np
 import pytest
 import torch
@@ -8,6 +14,17 @@ import torch
 from conftest import assert_close_bf16, bf16_bits, pkg_module, u8
 
 pytestmark = pytest.mark.gpu
+
+P_ROUND = 2.0 ** -8   # relative rounding of a probability to bf16
+
+
+def _check(O, got, q, k, v, what, **kw):
+    """got vs the oracle, with the bf16-probability allowance described above."""
+    ref = O.attention_reference(q, k, v, **kw)
+    env = O.attention_reference(q, k, np.abs(v), **kw)
+    if got.ndim == 2:
+        ref, env = ref.reshape(got.shape), env.reshape(got.shape)
+    assert_close_bf16(got, ref, what=what, extra=P_ROUND * env)
 
 
 def _cache_from_chunks(dev, n_chunks, chunk, H, D, seed, fmt="fp8", capacity=None):
@@ -27,9 +44,11 @@ def _cache_from_chunks(dev, n_chunks, chunk, H, D, seed, fmt="fp8", capacity=Non
 
 
 def _dequant(O, cache, n, fmt="fp8"):
-    dec = O.e4m3_decode if fmt == "fp8" else O.int8_decode
-    k = dec(u8(cache["k"][0, :n])) * cache["k_scale"][0, :n].cpu().numpy()
-    v = dec(u8(cache["v"][0, :n])) * cache["v_scale"][0, :n].cpu().numpy()
+    """The K/V the reference attends over: bf16(code * scale), the decode of
+    int8_kv_cache.py:88,204 feeding the attention at nomas_cpt.py:530-531."""
+    f = O.KV_FP8 if fmt == "fp8" else O.KV_INT8
+    k = O.bf16_bits_to_f32(O.kv_dequantize(u8(cache["k"][0, :n]), cache["k_scale"][0, :n].cpu().numpy(), f))
+    v = O.bf16_bits_to_f32(O.kv_dequantize(u8(cache["v"][0, :n]), cache["v_scale"][0, :n].cpu().numpy(), f))
     return k, v
 
 
@@ -55,8 +74,8 @@ def test_chunk_attention_small(O, dev, Lq, n_chunks, chunk, q_chunk0, fmt):
     out = ca.chunk_attention(q, cache, kv_len, q_pos0=q_pos0, chunk_len=chunk)
     kh, vh = _dequant(O, cache, kv_len, fmt)
     vis = O.block_causal_visible(np.arange(q_pos0, q_pos0 + Lq), np.arange(kv_len), chunk)
-    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kh, vh, visible=vis)
-    assert_close_bf16(out[0].float().cpu().numpy(), ref, what="chunk attention")
+    _check(O, out[0].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0])), kh, vh, "chunk attention",
+           visible=vis)
 
 
 def test_chunk_attention_with_bf16_tail(O, dev):
@@ -72,12 +91,11 @@ def test_chunk_attention_with_bf16_tail(O, dev):
     kh, vh = _dequant(O, cache, 2 * chunk)
     kall = np.concatenate([kh, O.bf16_bits_to_f32(bf16_bits(kc[0]))], 0)
     vall = np.concatenate([vh, O.bf16_bits_to_f32(bf16_bits(vc[0]))], 0)
-    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kall, vall)
-    assert_close_bf16(out[0].float().cpu().numpy(), ref, what="attention + tail")
+    _check(O, out[0].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0])), kall, vall, "attention + tail")
     # tail only (empty cache prefix)
     out2 = ca.chunk_attention(q, cache, 0, k_cur=kc, v_cur=vc)
-    ref2 = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0])), kall[2 * chunk:], vall[2 * chunk:])
-    assert_close_bf16(out2[0].float().cpu().numpy(), ref2, what="tail only")
+    _check(O, out2[0].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0])), kall[2 * chunk:],
+           vall[2 * chunk:], "tail only")
 
 
 def test_chunk_attention_config3_sampled_rows(O, dev):
@@ -94,8 +112,7 @@ def test_chunk_attention_config3_sampled_rows(O, dev):
     assert torch.isfinite(out.float()).all()
     rows = np.concatenate([np.arange(0, 32), np.arange(5400, 5432), np.arange(10768, 10800)])
     kh, vh = _dequant(O, cache, kv_len)
-    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh)
-    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="config 3")
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh, "config 3")
 
 
 def test_chunk_attention_two_chunk_queries_triangle(O, dev):
@@ -109,8 +126,8 @@ def test_chunk_attention_two_chunk_queries_triangle(O, dev):
     rows = np.concatenate([np.arange(10780, 10820), np.arange(21560, 21600)])
     kh, vh = _dequant(O, cache, 3 * chunk)
     vis = O.block_causal_visible(chunk + rows, np.arange(3 * chunk), chunk)
-    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh, visible=vis)
-    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="triangle")
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh, "triangle",
+           visible=vis)
 
 
 @pytest.mark.parametrize("Lq,kv_len,H", [(128, 86400, 24), (100, 20000, 4), (1, 5000, 2)])
@@ -128,8 +145,7 @@ def test_split_kv_decode_style(O, dev, Lq, kv_len, H):
     out = ca.chunk_attention(q, cache, kv_len)
     rows = np.arange(0, Lq, max(1, Lq // 16))
     kh, vh = _dequant(O, cache, kv_len)
-    ref = O.attention_reference(O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh)
-    assert_close_bf16(out[0, rows].float().cpu().numpy(), ref, what="split-kv")
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh, "split-kv")
 
 
 def test_attention_invariants(dev):
@@ -183,10 +199,9 @@ def test_causal_attention_with_cache_mp_matches_reference_semantics(O, dev):
         kall = np.concatenate([hist_k, cur_k], 0)
         vall = np.concatenate([hist_v, cur_v], 0)
         qall = np.concatenate([O.bf16_bits_to_f32(bf16_bits(t[0])) for t in q], 0)
-        ref = O.attention_reference(qall, kall, vall).reshape(Li + Lt, H * D)
         got = torch.cat([img[0], txt[0]], 0).float().cpu().numpy()
         assert img.shape == (1, Li, H * D) and txt.shape == (1, Lt, H * D)
-        assert_close_bf16(got, ref, what=f"cached attention step {step}")
+        _check(O, got, qall, kall, vall, f"cached attention step {step}")
         if update:
             assert mask[0, valid:valid + Li + Lt].all()
             valid += Li + Lt
