@@ -181,11 +181,14 @@ HN_DEVICE uint32_t pack_bf16(float a, float b) {
 // (tile-local). Each wave scales its 128 x 128 sub-tile, packs it to bf16 and
 // parks it in its own LDS slice; then it writes the slice out as 256-byte row
 // segments (16 lanes x 16 bytes per row, 4 rows per store).
-template <int MODE>
-HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_t n0, uint8_t* smem,
-                        int wave, int wm, int wn, int lane, int imax = 4, int jmax = 4) {
-    __syncthreads();  // the last K step's LDS reads are done (all waves)
-    uint8_t* ow = smem + wave * OUT_WAVE_BYTES;
+//
+// The per-row / per-column scales and the bias the lane needs (4 + 16 x 4 +
+// 16 x 4 values) are loaded in one batch up front: with one wave per SIMD
+// nothing else hides a load's latency, so loading them group by group would
+// expose it sixteen times.
+template <int MODE, int ACT>
+HN_DEVICE void epilogue_act(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_t n0, uint8_t* smem,
+                            int wave, int wm, int wn, int lane, int imax, int jmax) {
     float sam[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -193,23 +196,32 @@ HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_
         m = m < p.M ? m : p.M - 1;
         sam[j] = MODE == ROWCOL ? p.sa[m] : 1.0f;
     }
+    float4 sbn[4][4];
+    uint2 bias[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+            int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
+            n = n < p.N ? n : p.N - 4;  // stays in bounds; columns past N are not stored
+            sbn[i][vq] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            bias[i][vq] = make_uint2(0u, 0u);
+            if (MODE == ROWCOL) {
+                sbn[i][vq] = *reinterpret_cast<const float4*>(p.sb + n);
+                if (p.bias) bias[i][vq] = *reinterpret_cast<const uint2*>(p.bias + n);
+            }
+        }
+    __syncthreads();  // the last K step's LDS reads are done (all waves)
+    uint8_t* ow = smem + wave * OUT_WAVE_BYTES;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         if (i >= imax) continue;  // weight block wholly past N (wave-uniform)
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
-            int64_t n = n0 + wn * 128 + i * 32 + vq * 8 + (lane >> 5) * 4;
-            n = n < p.N ? n : p.N - 4;  // stays in bounds; columns past N are not stored
-            float sbn[4] = {1.0f, 1.0f, 1.0f, 1.0f}, bn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (MODE == ROWCOL) {
-                const float4 s4 = *reinterpret_cast<const float4*>(p.sb + n);
-                sbn[0] = s4.x; sbn[1] = s4.y; sbn[2] = s4.z; sbn[3] = s4.w;
-                if (p.bias) {
-                    const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
-                    bn[0] = bf16_bits_to_f32(bb.x & 0xffffu); bn[1] = bf16_bits_to_f32(bb.x >> 16);
-                    bn[2] = bf16_bits_to_f32(bb.y & 0xffffu); bn[3] = bf16_bits_to_f32(bb.y >> 16);
-                }
-            }
+            const float sb4[4] = {sbn[i][vq].x, sbn[i][vq].y, sbn[i][vq].z, sbn[i][vq].w};
+            const uint2 bb = bias[i][vq];
+            const float bn[4] = {bf16_bits_to_f32(bb.x & 0xffffu), bf16_bits_to_f32(bb.x >> 16),
+                                 bf16_bits_to_f32(bb.y & 0xffffu), bf16_bits_to_f32(bb.y >> 16)};
             const int nl = i * 32 + vq * 8 + (lane >> 5) * 4;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -217,8 +229,8 @@ HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_
                 float y[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    y[e] = fmaf(acc[i][j][vq * 4 + e], sam[j] * sbn[e], bn[e]);
-                    if (MODE == ROWCOL && p.act == HN_ACT_GELU_TANH) y[e] = gelu_tanh(y[e]);
+                    y[e] = fmaf(acc[i][j][vq * 4 + e], sam[j] * sb4[e], bn[e]);
+                    if (ACT == HN_ACT_GELU_TANH) y[e] = gelu_tanh(y[e]);
                 }
                 const int ml = j * 32 + (lane & 31);
                 *reinterpret_cast<uint2*>(ow + ml * OUT_ROW + nl * 2) =
@@ -237,7 +249,15 @@ HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_
         const uint4 v = *reinterpret_cast<const uint4*>(ow + ml * OUT_ROW + (lane & 15) * 16);
         if (m < p.M && nbase < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + nbase) = v;
     }
+}
 
+template <int MODE>
+HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_t n0, uint8_t* smem,
+                        int wave, int wm, int wn, int lane, int imax = 4, int jmax = 4) {
+    if (MODE == ROWCOL && p.act == HN_ACT_GELU_TANH)
+        epilogue_act<MODE, HN_ACT_GELU_TANH>(acc, p, m0, n0, smem, wave, wm, wn, lane, imax, jmax);
+    else
+        epilogue_act<MODE, HN_ACT_NONE>(acc, p, m0, n0, smem, wave, wm, wn, lane, imax, jmax);
 }
 
 template <int MODE>
