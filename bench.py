@@ -37,6 +37,7 @@ NS_M, NS_K, NS_N = 10800, 3072, 12288
 C1_M, C1_K, C1_N = 4096, 3072, 3072
 KV_H, KV_L, KV_D = 24, 10800, 128
 ATT_CHUNKS = 8
+ATT_LQ, ATT_LK = KV_L, ATT_CHUNKS * KV_L   # config 3: 10800 queries over 86400 cached keys
 
 
 def gemm_flops(m, k, n):
@@ -397,11 +398,76 @@ def cpu_baseline(seconds, log):
                 break
     tflops = gemm_flops(rows, NS_K, NS_N) * n / el / 1e12
     log(f"cpu baseline {tflops * 1e3:.2f} GFLOP/s over {n} x {rows} rows in {el:.1f} s")
-    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(blas[0]) if blas else cores,
-            "kind": "port",
-            "sample": f"{n} x {rows} token rows of the north-star linear ({rows}x{NS_K}x{NS_N}): "
-                      f"oracle per-token e4m3 quant (C) + dequantize-then-matmul (numpy float64 BLAS) "
-                      f"+ bias + GELU, {el:.1f} s"}
+    out = {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(blas[0]) if blas else cores,
+           "kind": "port",
+           "sample": f"{n} x {rows} token rows of the north-star linear ({rows}x{NS_K}x{NS_N}): "
+                     f"oracle per-token e4m3 quant (C) + dequantize-then-matmul (numpy float64 BLAS) "
+                     f"+ bias + GELU, {el:.1f} s"}
+    out["kv_write"] = cpu_kv_write(O, seconds / 4, log)
+    out["attention"] = cpu_attention(seconds / 2, cores, log)
+    return out
+
+
+def cpu_kv_write(O, seconds, log):
+    """Config-2 recipe on the host (the reference CPU branch, int8_kv_cache.py:149-158, with
+    448 and the e4m3 cast): the oracle's per-(token, head) quantizer in C, 1 thread, over
+    a 1350-token x 24-head sample of K (1/8 of config 2's K), scaled to config 2's bytes."""
+    import numpy as np
+    rng = np.random.default_rng(1)
+    L = KV_L // 8
+    gain = rng.uniform(0.5, 4.0, KV_H).astype(np.float32)
+    x = O.f32_to_bf16_bits((rng.standard_normal((1, L, KV_H, KV_D)) * gain[None, None, :, None]).astype(np.float32))
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.kv_quantize(x)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 200:
+            break
+    rows = n * L * KV_H
+    gbs = rows * (KV_D * 2 + KV_D + 4) / el / 1e9
+    us_config2 = 2 * KV_L * KV_H * (el / rows) * 1e6
+    log(f"cpu KV write {gbs:.2f} GB/s ({us_config2 / 1e3:.1f} ms for config 2's K and V)")
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "config2_ms_extrapolated": round(us_config2 / 1e3, 2),
+            "sample": f"{n} x [1, {L}, {KV_H}, {KV_D}] bf16 rows through the oracle's KV quantizer (C), {el:.1f} s"}
+
+
+def cpu_attention(seconds, cores, log):
+    """Config-3 reference path on the host (nomas_cpt.py:771-781, attn_mode="torch"): decode
+    the FP8 cache to bf16 with the reference's CPU branch (int8_kv_cache.py:202-204) and run
+    torch's CPU scaled_dot_product_attention, for one head and a 64-query slice over all
+    86 400 keys; TFLOP/s and the time extrapolated to config 3 (x 24 heads x 10800/64)."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    rng = np.random.default_rng(2)
+    Lk, Lq = ATT_LK, 64
+    codes = torch.from_numpy(rng.integers(0, 0x78, (2, Lk, KV_D), dtype=np.uint8)).view(torch.float8_e4m3fn)
+    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (2, Lk, 1)).astype(np.float32))
+    q = torch.randn(1, 1, Lq, KV_D).to(torch.bfloat16)
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        n, t0 = 0, time.perf_counter()
+        while True:
+            kv = (codes.float() * scales).to(torch.bfloat16)   # the reference's CPU decode
+            k, v = kv[0][None, None], kv[1][None, None]
+            F.scaled_dot_product_attention(q, k, v, scale=KV_D ** -0.5)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 50:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    flop = 4.0 * Lq * Lk * KV_D * n
+    tflops = flop / el / 1e12
+    ms3 = el / n * KV_H * (ATT_LQ / Lq) * 1e3
+    log(f"cpu attention {tflops * 1e3:.1f} GFLOP/s ({ms3 / 1e3:.0f} s extrapolated to config 3)")
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "reference path (torch CPU)",
+            "config3_s_extrapolated": round(ms3 / 1e3, 1),
+            "sample": f"{n} x (decode 2 x {Lk} x {KV_D} FP8 codes + bf16 SDPA of {Lq} queries over "
+                      f"{Lk} keys, one head), {el:.1f} s"}
 
 
 if __name__ == "__main__":
