@@ -2,10 +2,12 @@
 //
 //   O = softmax(Q K^T * scale) V,   K, V = code * per-(token, head) scale
 //
-// Work decomposition: one workgroup = 4 waves = 128 queries of one (batch,
-// head); each wave owns 32 queries (one 32-column MFMA block); two workgroups
-// share a CU (2 waves per SIMD). Keys stream through LDS in tiles of 64, two
-// stages. Each tile is dequantized once per workgroup as it is written to LDS,
+// Work decomposition: one workgroup = NW waves = 32 NW queries of one (batch,
+// head); each wave owns 32 queries (one 32-column MFMA block). Two shapes:
+// 4 waves (128 queries, two workgroups per CU) and 8 waves (256 queries, one
+// per CU); both put 2 waves on each SIMD, and the 8-wave shape dequantizes
+// each K/V tile once for twice the queries. Keys stream through LDS in tiles
+// of 64, two stages. Each tile is dequantized once per workgroup as it is written to LDS,
 // to the reference's own dequantized values: K = bf16(code * k_scale) and
 // V = bf16(code * v_scale) (fp32 product, rounded to nearest even), so the
 // MFMAs consume exactly the bf16 K/V the reference attends over, and no
@@ -36,10 +38,7 @@ namespace attn {
 
 constexpr int D = 128;
 constexpr int BKV = 64;            // keys per tile
-constexpr int NW = 4;              // waves per workgroup
-constexpr int NT = 64 * NW;
 constexpr int QW = 32;             // queries per wave
-constexpr int BQ = QW * NW;        // queries per workgroup
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
 // V^T tile: 128 dim rows of 64 bf16 keys (128 B) padded to 144 B = 9 16-byte
 // units, so 16 consecutive rows at one column fall in 16 different bank
@@ -53,6 +52,16 @@ constexpr int STAGE = K_BYTES + VT_BYTES;
 // Per-key scales of a tile in flight ([0, 64) K, [64, 128) V), two buffers.
 constexpr int SB_FLOATS = 2 * BKV;
 constexpr int SMEM = 2 * STAGE + 2 * SB_FLOATS * 4;
+
+// Workgroup shape for NW (4 or 8) waves.
+template <int NW>
+struct Shape {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static constexpr int NT = 64 * NW;   // threads
+    static constexpr int BQ = QW * NW;   // queries
+    static constexpr int KU = 512 / NT;  // 16-code K units per thread (64 keys x 8 units)
+    static constexpr int VD = 2048 / NT; // V dims per thread (64 keys x 128 dims, 4-key quads)
+};
 
 struct Params {
     const uint16_t* q;
@@ -108,12 +117,13 @@ HN_DEVICE uint32_t pack_bf16(float a, float b) {
 // ---------------------------------------------------------------------------
 // Tile loads and LDS writes.
 //
-// K: thread t owns units u = t + 256 i (i < 2): key u / 8, 16 dims at 16 (u % 8).
+// K: thread t owns units u = t + NT i (i < KU): key u / 8, 16 dims at 16 (u % 8).
 // V^T: thread t (wave w, lane λ) owns key quad qd = λ % 16 (keys quad_key(qd, j),
-// j < 4: the 8-byte half qd % 2 of column unit qd / 2) and dims 8 dg .. 8 dg + 7,
-// dg = λ / 16 + 4 w. Per 8-byte LDS write a 32-lane group covers 2 dim groups x
-// 16 quads, whose bank pairs (18 row + qd) mod 32 are all distinct (row pitch
-// 144 B); per global load each wave reads 16 keys x 32 contiguous bytes.
+// j < 4: the 8-byte half qd % 2 of column unit qd / 2) and the VD dims VD dg ..
+// VD dg + VD - 1 (v_group). Per 8-byte LDS write a 32-lane group covers 2 dim
+// groups 8 rows apart x 16 quads, whose bank pairs (18 row + qd) mod 32 are all
+// distinct (row pitch 144 B, 18 x 8 = 16 mod 32); per global load each wave
+// reads 16 keys x 4 VD contiguous bytes.
 // Scales: threads 0-63 load the K scale of key t, threads 64-127 the V scale
 // of key t - 64, into the tile's scale buffer.
 
@@ -122,12 +132,22 @@ HN_DEVICE int quad_key(int qd, int j) {
     return 16 * (qd >> 2) + 4 * ((qd >> 1) & 1) + 8 * (qd & 1) + j;
 }
 
+// Dim group of this thread's V^T quad: lanes 0-31 and 32-63 of a wave take
+// groups whose first rows are 8 apart.
+template <int NW>
+HN_DEVICE int v_group() {
+    const int w = threadIdx.x >> 6, hh = (threadIdx.x & 63) >> 4;
+    if constexpr (NW == 4) return 4 * w + hh;                       // 8 dims per group
+    else return 4 * w + 2 * (hh & 1) + (hh >> 1);                   // 4 dims per group
+}
+
 // Registers holding one cache tile between its global load and its LDS
 // write (issued about one tile ahead).
+template <int NW>
 struct CacheRegs {
-    uint4 k[2];
-    uint2 v[4];  // 8 codes (dims 8 dg ..) of quad key j
-    float s;     // one per-key scale (threads < 128)
+    uint4 k[Shape<NW>::KU];
+    uint32_t v[4][Shape<NW>::VD / 4];  // VD codes (dims VD dg ..) of quad key j
+    float s;                           // one per-key scale (threads < 128)
 };
 
 // Base addresses of a cache tile: uniform (scalar) pointers; the per-thread
@@ -152,12 +172,13 @@ HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t firs
 
 // Keys past the end of a short tile re-read the tile's last key (they are
 // masked out of the softmax).
-HN_DEVICE void load_k(const Params& p, CacheRegs& r, const TileBase& tb, int count) {
+template <int NW>
+HN_DEVICE void load_k(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int count) {
     const uint32_t t = threadIdx.x;
     const uint32_t last = (uint32_t)count - 1u;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t key = min((t >> 3) + 32u * i, last);
+    for (int i = 0; i < Shape<NW>::KU; ++i) {
+        const uint32_t key = min((t >> 3) + (uint32_t)(Shape<NW>::NT / 8) * i, last);
         r.k[i] = *reinterpret_cast<const uint4*>(tb.k + (key * (uint32_t)p.cs1 + (t & 7u) * 16u));
     }
     if (t < 2u * BKV) {
@@ -166,67 +187,86 @@ HN_DEVICE void load_k(const Params& p, CacheRegs& r, const TileBase& tb, int cou
     }
 }
 
-HN_DEVICE void load_v(const Params& p, CacheRegs& r, const TileBase& tb, int count) {
-    const int lam = threadIdx.x & 63;
-    const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
+template <int NW>
+HN_DEVICE void load_v(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int count) {
+    constexpr int VD = Shape<NW>::VD;
+    const int qd = threadIdx.x & 15, dg = v_group<NW>();
     const uint32_t last = (uint32_t)count - 1u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t key = min((uint32_t)quad_key(qd, j), last);
-        r.v[j] = *reinterpret_cast<const uint2*>(tb.v + (key * (uint32_t)p.cs1 + 8u * (uint32_t)dg));
+        const uint8_t* src = tb.v + (key * (uint32_t)p.cs1 + (uint32_t)(VD * dg));
+        if constexpr (VD == 8) {
+            const uint2 x = *reinterpret_cast<const uint2*>(src);
+            r.v[j][0] = x.x;
+            r.v[j][1] = x.y;
+        } else {
+            r.v[j][0] = *reinterpret_cast<const uint32_t*>(src);
+        }
     }
 }
 
 HN_DEVICE uint32_t word(const uint4& c, int q) { return q == 0 ? c.x : q == 1 ? c.y : q == 2 ? c.z : c.w; }
 
-// Dequantized K write, part i (0..7): unit i / 4, codes 4 (i % 4) .. +3 ->
-// two bf16 dwords of kd; every second part writes 16 bytes (8 dims).
-template <int FMT>
-HN_DEVICE void store_k_part(const CacheRegs& r, uint8_t* st, int i, const float (&ks)[2], uint32_t (&kd)[4]) {
-    const int un = i >> 2, q = i & 3;
-    const uint32_t w = word(r.k[un], q);
-    const float s = ks[un];
-    const f32x2 a = codes2_f32<FMT>(w, false), c = codes2_f32<FMT>(w, true);
-    kd[2 * (q & 1)] = pack_bf16(a[0] * s, a[1] * s);
-    kd[2 * (q & 1) + 1] = pack_bf16(c[0] * s, c[1] * s);
-    if (q & 1) {
-        const int u = threadIdx.x + NT * un;
-        *reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32 + (q >> 1) * 16) =
+// Dequantized K write, part i (0..7): the thread's codes 2 KU i .. +2 KU - 1
+// (unit code / 16) into bf16 dwords of kd; each completed run of 8 codes is
+// one 16-byte write (every second part with 2 units, every fourth with 1).
+template <int FMT, int NW>
+HN_DEVICE void store_k_part(const CacheRegs<NW>& r, uint8_t* st, int i, const float (&ks)[Shape<NW>::KU],
+                            uint32_t (&kd)[4]) {
+    constexpr int CP = 2 * Shape<NW>::KU;  // codes per part
+    const int code0 = CP * i, un = code0 >> 4, c = code0 & 15;
+#pragma unroll
+    for (int c2 = 0; c2 < CP / 2; ++c2) {
+        const int cc = c + 2 * c2;
+        const f32x2 a = codes2_f32<FMT>(word(r.k[un], cc >> 2), (cc & 2) != 0);
+        kd[(cc >> 1) & 3] = pack_bf16(a[0] * ks[un], a[1] * ks[un]);
+    }
+    if (((c + CP) & 7) == 0) {
+        const int u = threadIdx.x + Shape<NW>::NT * un;
+        *reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32 + ((c + CP - 8) >> 3) * 16) =
             make_uint4(kd[0], kd[1], kd[2], kd[3]);
     }
 }
 
-// The K scales of the thread's two units, from the tile's scale buffer.
-HN_DEVICE void k_scales(const float* sb, float (&ks)[2]) {
-    ks[0] = sb[threadIdx.x >> 3];
-    ks[1] = sb[(threadIdx.x >> 3) + 32];
+// The K scales of the thread's units, from the tile's scale buffer.
+template <int NW>
+HN_DEVICE void k_scales(const float* sb, float (&ks)[Shape<NW>::KU]) {
+#pragma unroll
+    for (int i = 0; i < Shape<NW>::KU; ++i) ks[i] = sb[(threadIdx.x >> 3) + (Shape<NW>::NT / 8) * i];
 }
 
-// Dequantized V^T write, part i (0..7): quad key j = i / 2, dims 4 (i % 2) ..
-// +3 of the thread's 8; keys (0, 1) and (2, 3) pair into bf16 dwords
-// (vd[2 d + pair], dim d), and parts 6 and 7 write dims 0-3 and 4-7 (8 bytes
-// = 4 keys each).
-template <int FMT>
-HN_DEVICE void store_v_part(const CacheRegs& r, uint8_t* st, int i, const float4& vs, float (&vp)[8],
-                            uint32_t (&vd)[16]) {
+// Dequantized V^T write, part i (0..7): quad key j = i / 2, dims VD/2 (i % 2)
+// .. + VD/2 - 1 of the thread's VD; keys (0, 1) and (2, 3) pair into bf16
+// dwords (vd[2 d + pair], dim d), and parts 6 and 7 write the two halves of
+// the dims (8 bytes = 4 keys each).
+template <int FMT, int NW>
+HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const float4& vs,
+                            float (&vp)[Shape<NW>::VD], uint32_t (&vd)[2 * Shape<NW>::VD]) {
+    constexpr int VD = Shape<NW>::VD, DP = VD / 2;
     const int j = i >> 1, hf = i & 1;
-    const uint32_t w = hf ? r.v[j].y : r.v[j].x;
-    const f32x2 a = codes2_f32<FMT>(w, false), c = codes2_f32<FMT>(w, true);
     const float s = j == 0 ? vs.x : j == 1 ? vs.y : j == 2 ? vs.z : vs.w;
-    const float x[4] = {a[0] * s, a[1] * s, c[0] * s, c[1] * s};
+    float x[DP];
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) {
-        const int d = 4 * hf + dd;
+    for (int c2 = 0; c2 < DP / 2; ++c2) {
+        const int code = DP * hf + 2 * c2;
+        const f32x2 a = codes2_f32<FMT>(r.v[j][code >> 2], (code & 2) != 0);
+        x[2 * c2] = a[0] * s;
+        x[2 * c2 + 1] = a[1] * s;
+    }
+#pragma unroll
+    for (int dd = 0; dd < DP; ++dd) {
+        const int d = DP * hf + dd;
         if (j & 1) vd[2 * d + (j >> 1)] = pack_bf16(vp[d], x[dd]);
         else vp[d] = x[dd];
     }
     if (j == 3) {
-        const int lam = threadIdx.x & 63;
-        const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
+        const int qd = threadIdx.x & 15, dg = v_group<NW>();
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-            const int d = 4 * hf + dd;
-            *reinterpret_cast<uint2*>(st + K_BYTES + (8 * dg + d) * VTROW + 8 * qd) = make_uint2(vd[2 * d], vd[2 * d + 1]);
+        for (int dd = 0; dd < DP; ++dd) {
+            const int d = DP * hf + dd;
+            *reinterpret_cast<uint2*>(st + K_BYTES + (VD * dg + d) * VTROW + 8 * qd) =
+                make_uint2(vd[2 * d], vd[2 * d + 1]);
         }
     }
 }
@@ -238,18 +278,18 @@ HN_DEVICE float4 v_scales(const float* sb) {
 }
 
 // Whole-tile write (prologue), scales from the tile's scale buffer.
-template <int FMT>
-HN_DEVICE void store_tile(const CacheRegs& r, uint8_t* st, const float* sb) {
-    float ks[2];
-    k_scales(sb, ks);
+template <int FMT, int NW>
+HN_DEVICE void store_tile(const CacheRegs<NW>& r, uint8_t* st, const float* sb) {
+    float ks[Shape<NW>::KU];
+    k_scales<NW>(sb, ks);
     const float4 vs = v_scales(sb);
     uint32_t kd[4];
-    float vp[8];
-    uint32_t vd[16];
+    float vp[Shape<NW>::VD];
+    uint32_t vd[2 * Shape<NW>::VD];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        store_k_part<FMT>(r, st, i, ks, kd);
-        store_v_part<FMT>(r, st, i, vs, vp, vd);
+        store_k_part<FMT, NW>(r, st, i, ks, kd);
+        store_v_part<FMT, NW>(r, st, i, vs, vp, vd);
     }
 }
 
@@ -257,11 +297,12 @@ HN_DEVICE void store_tile(const CacheRegs& r, uint8_t* st, const float* sb) {
 // same thread-to-location mapping as the cache writes (so it cleanly
 // replaces what those wrote to the same stage). Not prefetched: it is at most
 // one chunk of the keys.
+template <int NW>
 HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int u = t + NT * i;
+    for (int i = 0; i < Shape<NW>::KU; ++i) {
+        const int u = t + Shape<NW>::NT * i;
         const int j = min(u >> 3, count - 1);
         const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (u & 7) * 16;
         const uint4 lo = *reinterpret_cast<const uint4*>(src);
@@ -272,25 +313,31 @@ HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first,
     }
 }
 
+template <int NW>
 HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
-    const int lam = threadIdx.x & 63;
-    const int qd = lam & 15, dg = (lam >> 4) + 4 * (threadIdx.x >> 6);
-    uint4 w[4];  // dims 8 dg .. 8 dg + 7 of quad key j (bf16)
+    constexpr int VD = Shape<NW>::VD;
+    const int qd = threadIdx.x & 15, dg = v_group<NW>();
+    uint32_t w[4][VD / 2];  // dims VD dg .. + VD - 1 of quad key j (bf16 pairs)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = min(quad_key(qd, j), count - 1);
-        w[j] = *reinterpret_cast<const uint4*>(p.vcur + b * p.us0 + (first + key) * p.us1 + h * p.us2 + 8 * dg);
+        const uint16_t* src = p.vcur + b * p.us0 + (first + key) * p.us1 + h * p.us2 + VD * dg;
+        if constexpr (VD == 8) {
+            const uint4 x = *reinterpret_cast<const uint4*>(src);
+            w[j][0] = x.x; w[j][1] = x.y; w[j][2] = x.z; w[j][3] = x.w;
+        } else {
+            const uint2 x = *reinterpret_cast<const uint2*>(src);
+            w[j][0] = x.x; w[j][1] = x.y;
+        }
     }
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
+    for (int d = 0; d < VD; ++d) {
         uint32_t o[2];
+        const uint32_t sh = (d & 1) * 16;
 #pragma unroll
-        for (int pr = 0; pr < 2; ++pr) {
-            const uint32_t a = word(w[2 * pr], d >> 1), c = word(w[2 * pr + 1], d >> 1);
-            const uint32_t sh = (d & 1) * 16;
-            o[pr] = ((a >> sh) & 0xffffu) | (((c >> sh) & 0xffffu) << 16);
-        }
-        *reinterpret_cast<uint2*>(st + K_BYTES + (8 * dg + d) * VTROW + 8 * qd) = make_uint2(o[0], o[1]);
+        for (int pr = 0; pr < 2; ++pr)
+            o[pr] = ((w[2 * pr][d >> 1] >> sh) & 0xffffu) | (((w[2 * pr + 1][d >> 1] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<uint2*>(st + K_BYTES + (VD * dg + d) * VTROW + 8 * qd) = make_uint2(o[0], o[1]);
     }
 }
 
@@ -420,21 +467,21 @@ HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, bf16x8 (&pf
 // row and column in the stage) beside the raw max of the next block (s) and,
 // per STORE (1: K, 2: V^T), half of the write of the prefetched tile to stage
 // nst with the scales of buffer sb. Returns the next block's raw max (pair-wide).
-template <int FMT, int STORE>
+template <int FMT, int NW, int STORE>
 HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (&o)[4], const f32x16& s,
-                       const CacheRegs& r, uint8_t* nst, const float* sb) {
+                       const CacheRegs<NW>& r, uint8_t* nst, const float* sb) {
     // operand i (= 4 tt + db): dim block db, 16-key slice 2 kb + tt
     bf16x8 vf[8];
     vf[0] = ld_bf16x8(va + 64 * kb);
     vf[1] = ld_bf16x8(va + 64 * kb + 32 * VTROW);
-    float ks[2] = {0.0f, 0.0f};
+    float ks[Shape<NW>::KU] = {};
     float4 vs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (STORE == 1) k_scales(sb, ks);
+    if (STORE == 1) k_scales<NW>(sb, ks);
     if (STORE == 2) vs = v_scales(sb);
     float mx = -INFINITY;
     uint32_t kd[4];
-    float vp[8];
-    uint32_t vd[16];
+    float vp[Shape<NW>::VD];
+    uint32_t vd[2 * Shape<NW>::VD];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int tt = i >> 2, db = i & 3;
@@ -445,15 +492,16 @@ HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 
         o[db] = mfma_bf16(vf[i], pf[tt], o[db]);
         mx = fmaxf(mx, fmaxf(s[2 * i], s[2 * i + 1]));
         pin(mx);
-        if (STORE == 1) store_k_part<FMT>(r, nst, i, ks, kd);
-        if (STORE == 2) store_v_part<FMT>(r, nst, i, vs, vp, vd);
+        if (STORE == 1) store_k_part<FMT, NW>(r, nst, i, ks, kd);
+        if (STORE == 2) store_v_part<FMT, NW>(r, nst, i, vs, vp, vd);
         __builtin_amdgcn_sched_barrier(0);
     }
     return pair_max(mx);
 }
 
-template <int FMT>
-__global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
+template <int FMT, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
+    constexpr int BQ = Shape<NW>::BQ;
     __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
     float* const sbuf = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][128]
 
@@ -556,7 +604,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
     // block 0) at column unit `half` (slice 0).
     const uint32_t ka_off = col * KROW + 16 * half;
     const uint32_t va_off = K_BYTES + col * VTROW + 16 * half;
-    CacheRegs regs;
+    CacheRegs<NW> regs;
     regs.s = 0.0f;
 
     // Software pipeline over half tiles. Per tile u = t - t_begin (stage
@@ -578,22 +626,22 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
         {
             if (g.cache) {
                 const TileBase tb = tile_base(p, b, h, g.first);
-                load_k(p, regs, tb, g.count);
-                load_v(p, regs, tb, g.count);
+                load_k<NW>(p, regs, tb, g.count);
+                load_v<NW>(p, regs, tb, g.count);
                 __builtin_amdgcn_s_waitcnt(0);
                 if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
                 __syncthreads();
-                store_tile<FMT>(regs, smem, sbuf);
+                store_tile<FMT, NW>(regs, smem, sbuf);
             } else {
-                copy_tail_k(p, b, h, g.first, g.count, smem);
-                copy_tail_v(p, b, h, g.first, g.count, smem);
+                copy_tail_k<NW>(p, b, h, g.first, g.count, smem);
+                copy_tail_v<NW>(p, b, h, g.first, g.count, smem);
             }
             if (t_begin + 1 < t_end) {
                 const Geom g1 = geom(t_begin + 1);
                 if (g1.cache) {
                     const TileBase tb = tile_base(p, b, h, g1.first);
-                    load_k(p, regs, tb, g1.count);
-                    load_v(p, regs, tb, g1.count);
+                    load_k<NW>(p, regs, tb, g1.count);
+                    load_v<NW>(p, regs, tb, g1.count);
                 }
             }
             // Everything issued so far (the Q fragments included) has landed;
@@ -621,22 +669,22 @@ __global__ __launch_bounds__(NT, 2) void attn_fp8kv_kernel(Params p) {
             // K of tile t + 1 from the prefetch registers (a tail tile or the
             // end of the range is handled right after: the K rows of the stage
             // are not read before the barrier).
-            mxb = step_b<FMT, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
+            mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
             if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
-            if (has_next && !gn.cache) copy_tail_k(p, b, h, gn.first, gn.count, nst);
-            if (fetch2 && g2.cache) load_k(p, regs, tile_base(p, b, h, g2.first), g2.count);
+            if (has_next && !gn.cache) copy_tail_k<NW>(p, b, h, gn.first, gn.count, nst);
+            if (fetch2 && g2.cache) load_k<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
             __syncthreads();
 
             // ---- half 1 (on the last tile the S block of "tile t + 1" reads
             // stale LDS; its result is never used)
             rebase(mxb, c, m, l, o);
             sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
-            mxa = step_b<FMT, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
+            mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
             if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
-            if (has_next && !gn.cache) copy_tail_v(p, b, h, gn.first, gn.count, nst);
+            if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
             if (fetch2 && g2.cache) {
                 if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                load_v(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                load_v<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
             }
             __syncthreads();
             g = gn;
@@ -708,18 +756,13 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restri
 
 using namespace hn;
 
-// Split selection: a launch wants at least two workgroups per CU (two fit per
-// CU by LDS and registers). When (batch x heads x query tiles) falls short, the
-// key range of each query tile is split so that the grid fills the device
-// (the decode-style case: a few hundred queries over a long cache); each split
-// keeps at least 16 key tiles.
-static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t cur_len) {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-    }
-    const int64_t work = B * H * ((Lq + attn::BQ - 1) / attn::BQ);
+// Split selection for the 4-wave kernel: a launch wants at least two
+// workgroups per CU (two fit per CU by LDS and registers). When (batch x heads
+// x query tiles) falls short, the key range of each query tile is split so
+// that the grid fills the device (the decode-style case: a few hundred
+// queries over a long cache); each split keeps at least 16 key tiles.
+static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t cur_len, int cus) {
+    const int64_t work = B * H * ((Lq + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ);
     const int64_t target = 2LL * cus;
     if (work <= 0 || work >= target) return 1;
     const int64_t tiles = (kv_len + cur_len + attn::BKV - 1) / attn::BKV;
@@ -731,12 +774,92 @@ static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t
     return sp > 1 ? (int)sp : 1;
 }
 
+// Launch plan: query rows [0, rows8) go to the 8-wave kernel (whole 256-query
+// tiles, no key split), rows [rows8, Lq) to the 4-wave kernel with `splits`
+// key-range splits.
+//
+// Model, in units of one full round of 4-wave workgroups (2 per CU, 128
+// queries each, which takes as long per key tile as one round of 8-wave
+// workgroups, 1 per CU, 256 queries each -- the 8-wave round measures 0.92 of
+// it at 86400 keys, so K8_ROUND = 0.92):
+//   4-wave only: ceil(n4 / 2C) rounds, n4 = B H ceil(Lq / 128);
+//   8-wave:      ceil(n8 / C) K8_ROUND rounds, n8 = B H floor(Lq / 256), plus
+//                the leftover rows on the 4-wave kernel, split sp ways:
+//                ceil(nr sp / 2C) / sp rounds.
+// The 8-wave kernel is used only when it fills every CU at least once
+// (n8 >= C) and the model says it is faster: a partial last round of 1-per-CU
+// workgroups idles half the SIMD slots a 4-wave round would keep busy.
+struct AttnPlan {
+    int64_t rows8;
+    int splits;
+};
+
+static AttnPlan attn_plan(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t cur_len) {
+    constexpr double K8_ROUND = 0.92;
+    const int cus = device_cus();
+    AttnPlan plan{0, 1};
+    const int64_t bh = B * H;
+    const int64_t n8 = bh * (Lq / attn::Shape<8>::BQ);
+    if (n8 >= cus) {
+        const int64_t n4 = bh * ((Lq + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ);
+        const double r4 = (double)((n4 + 2 * cus - 1) / (2 * cus));
+        double r8 = K8_ROUND * (double)((n8 + cus - 1) / cus);
+        const int64_t rows8 = (Lq / attn::Shape<8>::BQ) * attn::Shape<8>::BQ;
+        const int64_t rest = Lq - rows8;
+        if (rest > 0) {
+            const int sp = attn_splits(B, rest, H, kv_len, cur_len, cus);
+            const int64_t nr = bh * ((rest + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ) * sp;
+            r8 += (double)((nr + 2 * cus - 1) / (2 * cus)) / sp;
+        }
+        if (r8 < r4) plan.rows8 = rows8;
+    }
+    plan.splits = attn_splits(B, Lq - plan.rows8, H, kv_len, cur_len, cus);
+    return plan;
+}
+
+static int64_t plan_workspace(const AttnPlan& plan, int64_t B, int64_t Lq, int64_t H) {
+    if (plan.splits <= 1) return 0;
+    return (int64_t)plan.splits * B * H * (Lq - plan.rows8) * (attn::D + 2) * (int64_t)sizeof(float);
+}
+
 extern "C" int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
                                                 int64_t kv_len, int64_t cur_len) {
     if (B <= 0 || Lq <= 0 || H <= 0 || D != attn::D || kv_len < 0 || cur_len < 0) return 0;
-    const int sp = attn_splits(B, Lq, H, kv_len, cur_len);
-    if (sp <= 1) return 0;
-    return (int64_t)sp * B * H * Lq * (D + 2) * (int64_t)sizeof(float);
+    return plan_workspace(attn_plan(B, Lq, H, kv_len, cur_len), B, Lq, H);
+}
+
+// One launch of the NW-wave kernel over query rows [row0, row0 + rows) of p's
+// problem (p.Lq = all rows), with `sp` key-range splits merged through the
+// workspace by attn_combine_kernel.
+template <int NW>
+static int launch_rows(attn::Params p, int64_t B, int64_t row0, int64_t rows, int sp, void* workspace,
+                       hipStream_t stream) {
+    constexpr int BQ = attn::Shape<NW>::BQ;
+    p.q += row0 * p.qs1;
+    p.out += row0 * p.os1;
+    p.q_pos0 += row0;
+    p.Lq = rows;
+    const int64_t qt = (rows + BQ - 1) / BQ;
+    const int64_t work = B * p.H * qt * sp;
+    HN_REQUIRE(work <= 0x3fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too much work for one launch");
+    p.q_tiles = (int)qt;
+    p.splits = sp;
+    p.work = (int)work;
+    p.per_xcd = (int)((work + 7) / 8);
+    p.ws_o = sp > 1 ? (float*)workspace : nullptr;
+    p.ws_ml = sp > 1 ? (float*)workspace + (int64_t)sp * B * p.H * rows * attn::D : nullptr;
+    const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
+    if (p.fmt == HN_KV_FP8)
+        attn::attn_fp8kv_kernel<HN_KV_FP8, NW><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
+    else
+        attn::attn_fp8kv_kernel<HN_KV_INT8, NW><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
+    int rc = check_launch("hn_attn_fp8kv");
+    if (rc != HN_OK || sp <= 1) return rc;
+    const int64_t nrows = B * p.H * rows;
+    HN_REQUIRE(nrows <= 0x7fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too many rows to combine");
+    attn::attn_combine_kernel<<<(unsigned)nrows, attn::D, 0, stream>>>(p.ws_o, p.ws_ml, sp, nrows, rows, p.H,
+                                                                       p.out, p.os0, p.os1, p.os2);
+    return check_launch("hn_attn_fp8kv (combine)");
 }
 
 extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
@@ -795,29 +918,14 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
     p.q_pos0 = q_pos0; p.chunk = chunk_len;
     p.scale_log2 = softmax_scale * 1.4426950408889634f;
     p.fmt = fmt;
-    const int64_t qt = (Lq + attn::BQ - 1) / attn::BQ;
-    const int sp = attn_splits(B, Lq, H, kv_len, cur_len);
-    const int64_t need = sp > 1 ? (int64_t)sp * B * H * Lq * (D + 2) * (int64_t)sizeof(float) : 0;
+    const AttnPlan plan = attn_plan(B, Lq, H, kv_len, cur_len);
+    const int64_t need = plan_workspace(plan, B, Lq, H);
     HN_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))), HN_E_ARG,
                "hn_attn_fp8kv: workspace smaller than hn_attn_fp8kv_workspace_size() or misaligned");
-    const int64_t work = B * H * qt * sp;
-    HN_REQUIRE(work <= 0x3fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too much work for one launch");
-    p.q_tiles = (int)qt;
-    p.splits = sp;
-    p.work = (int)work;
-    p.per_xcd = (int)((work + 7) / 8);
-    p.ws_o = sp > 1 ? (float*)workspace : nullptr;
-    p.ws_ml = sp > 1 ? (float*)workspace + (int64_t)sp * B * H * Lq * D : nullptr;
-    const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    if (fmt == HN_KV_FP8)
-        attn::attn_fp8kv_kernel<HN_KV_FP8><<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
-    else
-        attn::attn_fp8kv_kernel<HN_KV_INT8><<<grid, attn::NT, 0, (hipStream_t)stream>>>(p);
-    int rc = check_launch("hn_attn_fp8kv");
-    if (rc != HN_OK || sp <= 1) return rc;
-    const int64_t rows = B * H * Lq;
-    HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too many rows to combine");
-    attn::attn_combine_kernel<<<(unsigned)rows, attn::D, 0, (hipStream_t)stream>>>(
-        p.ws_o, p.ws_ml, sp, rows, Lq, H, (uint16_t*)out, os[0], os[1], os[2]);
-    return check_launch("hn_attn_fp8kv (combine)");
+    const hipStream_t st = (hipStream_t)stream;
+    if (plan.rows8 > 0) {
+        const int rc = launch_rows<8>(p, B, 0, plan.rows8, 1, nullptr, st);
+        if (rc != HN_OK || plan.rows8 == Lq) return rc;
+    }
+    return launch_rows<4>(p, B, plan.rows8, Lq - plan.rows8, plan.splits, workspace, st);
 }

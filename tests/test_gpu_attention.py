@@ -130,6 +130,67 @@ def test_chunk_attention_two_chunk_queries_triangle(O, dev):
            visible=vis)
 
 
+# The 8-wave workgroup shape (256 queries) takes the whole 256-query tiles of a
+# launch once they fill every CU (B H floor(Lq / 256) >= 256 on MI355X); rows
+# past the last whole tile go to the 4-wave shape in a second launch.
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_eight_wave_tiles_causal_triangle(O, dev, fmt):
+    """H 128 x 2 whole tiles: every row on the 8-wave shape. Q covers chunks 1-3
+    of a 4-chunk cache, so tiles straddle chunk boundaries (per-element mask)."""
+    print(f"case attn 8-wave triangle {fmt}", flush=True)
+    ca = pkg_module("cache_attention")
+    H, D, chunk, n, Lq, q_pos0 = 128, 128, 200, 4, 512, 200
+    cache = _cache_from_chunks(dev, n, chunk, H, D, 600, fmt)
+    kv_len = n * chunk
+    q = _q(dev, Lq, H, D, 61)
+    out = ca.chunk_attention(q, cache, kv_len, q_pos0=q_pos0, chunk_len=chunk)
+    kh, vh = _dequant(O, cache, kv_len, fmt)
+    vis = O.block_causal_visible(np.arange(q_pos0, q_pos0 + Lq), np.arange(kv_len), chunk)
+    _check(O, out[0].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0])), kh, vh, "8-wave triangle",
+           visible=vis)
+
+
+def test_eight_wave_tiles_with_bf16_tail(O, dev):
+    """Denoising-pass form on the 8-wave shape: 2 FP8 chunks + the current
+    chunk's bf16 K/V (tail tiles copied into LDS by 512 threads)."""
+    print("case attn 8-wave tail", flush=True)
+    ca = pkg_module("cache_attention")
+    H, D, chunk = 64, 128, 1024
+    cache = _cache_from_chunks(dev, 2, chunk, H, D, 21)
+    g = torch.Generator(device=dev).manual_seed(22)
+    kc = (torch.randn(1, chunk, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    vc = (torch.randn(1, chunk, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+    q = _q(dev, chunk, H, D, 23)
+    out = ca.chunk_attention(q, cache, 2 * chunk, k_cur=kc, v_cur=vc)
+    rows = np.arange(0, chunk, 3)
+    kh, vh = _dequant(O, cache, 2 * chunk)
+    kall = np.concatenate([kh, O.bf16_bits_to_f32(bf16_bits(kc[0]))], 0)
+    vall = np.concatenate([vh, O.bf16_bits_to_f32(bf16_bits(vc[0]))], 0)
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kall, vall,
+           "8-wave + tail")
+
+
+def test_eight_wave_tiles_with_split_remainder(O, dev):
+    """Lq 1100 = 4 whole 256-query tiles + 76 rows, H 64, 16384 keys: rows < 1024
+    on the 8-wave shape, the last 76 on the 4-wave shape with the key range
+    split (workspace + combine, offset into the output)."""
+    print("case attn 8-wave + split remainder", flush=True)
+    lib = pkg_module("_lib").load()
+    H, D, chunk, n, Lq = 64, 128, 4096, 4, 1100
+    kv_len = n * chunk
+    ws = lib.hn_attn_fp8kv_workspace_size(1, Lq, H, D, kv_len, 0)
+    assert 0 < ws <= 16 * H * (Lq - 1024) * (D + 2) * 4   # only the remainder rows are split
+    ca = pkg_module("cache_attention")
+    cache = _cache_from_chunks(dev, n, chunk, H, D, 31)
+    q = _q(dev, Lq, H, D, 32)
+    out = ca.chunk_attention(q, cache, kv_len, q_pos0=(n - 1) * chunk, chunk_len=chunk)
+    rows = np.concatenate([np.arange(0, 16), np.arange(1000, 1100)])
+    kh, vh = _dequant(O, cache, kv_len)
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh,
+           "8-wave + split remainder")
+
+
 @pytest.mark.parametrize("Lq,kv_len,H", [(128, 86400, 24), (100, 20000, 4), (1, 5000, 2)])
 def test_split_kv_decode_style(O, dev, Lq, kv_len, H):
     """Few queries over a long cache: the key range is split across workgroups
