@@ -410,36 +410,37 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// Row/column-scaled kernel with a five-stage pipeline.
+// Row/column-scaled kernel: 128-byte K steps through five single-operand LDS
+// buffers.
 //
-// One wave per SIMD holds the 128 x 128 accumulator, so nothing else on the
-// SIMD hides memory latency: the K loop itself must. Stages here are 64 bytes
-// of K (A and B, 16 KB each = 32 KB), and five of them fill the 160 KB of LDS.
-// Stage s is requested four K steps before it is consumed, so each DMA has
-// three full K steps (about 3 x 1000 MFMA cycles) to arrive -- L2 misses that
-// go to the Infinity Cache or HBM included. The 16 MFMAs of a K step are
-// split in two halves around the per-step wait + barrier: the first half
-// runs on fragments already in registers while the wave waits, the second
-// half covers the LDS reads of the next step's fragments.
-constexpr int P_BK = 64;
-constexpr int P_STAGES = 5;
-constexpr int P_TILE = BM * P_BK;            // one operand, 16 KB
-constexpr int P_STAGE = 2 * P_TILE;          // A + B, 32 KB
-constexpr int P_SMEM = P_STAGES * P_STAGE;   // 160 KB
-static_assert(P_SMEM >= 4 * OUT_WAVE_BYTES, "epilogue staging must fit in the stage buffers");
-constexpr int P_DMA_PER_STAGE = 8;           // global_load_lds per wave per stage (4 A + 4 B)
-
-// 16-byte chunk c (0..3) of 64-byte LDS row r sits at position c ^ ((r >> 2) & 3):
-// 16 consecutive rows then cover all 16 bank groups of a 256-byte LDS cycle
-// (row r starts at bank group 4 (r & 3)).
-HN_DEVICE int pswz(int row, int chunk) { return row * P_BK + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// The stage DMA costs per cache line touched: one CU moves a 32 KB stage of
+// 128-byte row segments in about 810 cycles, but one of 64-byte segments (half
+// lines) in about 1360 -- more than the 1024 MFMA cycles a 64-byte K step of a
+// 256 x 256 tile takes. So every LDS buffer holds whole lines: one operand's
+// 256 rows x 128 bytes (32 KB, 16-byte chunks swizzled as swz()). Five buffers
+// fill the 160 KB of LDS; load L(i) -- A of K step i / 2 for even i, B for odd
+// i -- goes to buffer i % 5.
+//
+// K step k (128 bytes) runs as two halves of 16 MFMAs, one per 64-byte K slice,
+// each interleaved with the 16 LDS reads of the next slice's fragments:
+//   half 0: MFMAs on slice (k, 0); reads of slice (k, 1)
+//   mid:    wait for step k + 1's buffers and barrier; step k's buffers are
+//           then free (their last reads completed before the barrier)
+//   half 1: MFMAs on slice (k, 1); reads of slice (k + 1, 0); the loads
+//           L(2k + 5) = B(k + 2) and L(2k + 6) = A(k + 3) into step k's
+//           buffers, one 1 KB DMA per MFMA
+// B of a step is requested about one step (32 MFMAs) before its wait, A two
+// steps; with that lead the waits measure ~0 cycles per tile.
+constexpr int R_BUFS = 5;
+constexpr int R_BUF = BM * BK;            // one operand of one K step, 32 KB
+constexpr int R_SMEM = R_BUFS * R_BUF;    // 160 KB
+static_assert(R_SMEM >= 4 * OUT_WAVE_BYTES, "epilogue staging must fit in the stage buffers");
 
 // Stage loads use global_load_lds with a scalar base: the address is
 // sbase (SGPR pair: operand + tile row0 * K + k0) + voff (per-lane 32-bit
 // offset of the lane's row and chunk inside the tile, fixed for the tile), and
 // the LDS destination M0 is scalar too. Issuing a 1 KB load is then one s_mov
-// and the load -- no per-load vector address arithmetic or readfirstlane, so
-// the eight loads of a K step cost a few dozen issue cycles.
+// and the load -- no per-load vector address arithmetic or readfirstlane.
 HN_DEVICE void dma_16B_sbase(const uint8_t* sbase, uint32_t voff, uint32_t lds) {
     asm volatile(
         "s_mov_b32 m0, %2\n\t"
@@ -449,67 +450,38 @@ HN_DEVICE void dma_16B_sbase(const uint8_t* sbase, uint32_t voff, uint32_t lds) 
         : "memory", "m0");
 }
 
-// Per-lane offsets of a wave's four 1 KB regions (16 rows of 64 bytes) of one
-// 256 x 64 stage operand. Lane l lands at row l / 4, position l % 4 of region
-// wave * 4 + q and fetches the logical chunk that position holds. Rows past
-// the operand's end are clamped to its last row: in bounds, never stored.
-HN_DEVICE void stage_offsets(uint32_t (&off)[4], int64_t row0, int64_t rows, int64_t K, int wave,
-                             int lane) {
+// Per-lane offsets of a wave's eight 1 KB regions (8 rows of 128 bytes) of one
+// 256 x 128 buffer. Lane l lands at row l / 8, physical chunk l % 8 of region
+// wave * 8 + q and fetches the logical chunk that position holds (the swizzle
+// is an involution). Rows past the operand's end are clamped to its last row:
+// in bounds, never stored.
+HN_DEVICE void buffer_offsets(uint32_t (&off)[8], int64_t row0, int64_t rows, int64_t K, int wave, int lane) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = (wave * 4 + q) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 2) & 3);
+    for (int q = 0; q < 8; ++q) {
+        const int r = (wave * 8 + q) * 8 + (lane >> 3);
+        const int c = swz_pos(r, lane & 7);
         const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
         off[q] = (uint32_t)((row - row0) * K + (c << 4));
     }
 }
 
-HN_DEVICE i32x8 pread_frag(const uint8_t* lds, int row, int lane) {
-    const int c0 = (lane >> 5) * 2;
-    const uint4 lo = *reinterpret_cast<const uint4*>(lds + pswz(row, c0));
-    const uint4 hi = *reinterpret_cast<const uint4*>(lds + pswz(row, c0 + 1));
-    i32x8 f;
-    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
-    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
-    return f;
+// The fragments of K slice kh of step buffers (a_buf, b_buf).
+HN_DEVICE void read_slice(Frags& f, const uint8_t* a_buf, const uint8_t* b_buf, int kh, int wm, int wn,
+                          int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.b[i] = read_frag(b_buf, wn * 128 + i * 32 + (lane & 31), kh, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.a[j] = read_frag(a_buf, wm * 128 + j * 32 + (lane & 31), kh, lane);
 }
 
-HN_DEVICE void read_pfrags(Frags& f, const uint8_t* st, int wm, int wn, int lane) {
+// mfma_slice for an edge tile: only blocks inside the matrix (wave-uniform tests).
+HN_DEVICE void mfma_slice_partial(f32x16 (&acc)[4][4], const Frags& f, int imax, int jmax) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f.b[i] = pread_frag(st + P_TILE, wn * 128 + i * 32 + (lane & 31), lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.a[j] = pread_frag(st, wm * 128 + j * 32 + (lane & 31), lane);
-}
-
-// MFMAs of weight blocks i in [I0, I0 + 2) against all four activation blocks.
-template <int I0>
-HN_DEVICE void mfma_half(f32x16 (&acc)[4][4], const Frags& f) {
-#pragma unroll
-    for (int i = I0; i < I0 + 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
-}
-
-// mfma_half for an edge tile: only blocks inside the matrix (wave-uniform tests).
-template <int I0>
-HN_DEVICE void mfma_half_partial(f32x16 (&acc)[4][4], const Frags& f, int imax, int jmax) {
-#pragma unroll
-    for (int i = I0; i < I0 + 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (i < imax && j < jmax) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
 }
-
-// Wait until at most `stages` of this wave's stage loads are still in flight.
-HN_DEVICE void wait_stages_in_flight(int stages) {
-    switch (stages) {
-        case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-        case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-        case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    }
-}
-static_assert(P_DMA_PER_STAGE == 8, "wait_stages_in_flight counts 8 loads per stage");
 
 // Work item (XCD x = id % 8, position i = id / 8 in that XCD's queue) -> tile.
 // An XCD's queue holds its share of the full tiles, in groups of GROUP_M tile
@@ -545,7 +517,7 @@ HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) {
 }
 
 __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[P_SMEM];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[R_SMEM];
     int tm, tn;
     if (!tile_of(p, blockIdx.x, tm, tn)) return;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -553,13 +525,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave & 1, wn = wave >> 1;
-    const int KT = (int)(p.K / P_BK);
+    const int KT = (int)(p.K / BK);
     const uint8_t* const a_tile = p.a + m0 * p.K;
     const uint8_t* const b_tile = p.b + n0 * p.K;
-    uint32_t off_a[4], off_b[4];
-    stage_offsets(off_a, m0, p.M, p.K, wave, lane);
-    stage_offsets(off_b, n0, p.N, p.K, wave, lane);
-    const uint32_t lds_base = lds_addr(smem) + wave * 4 * 1024;
+    uint32_t off_a[8], off_b[8];
+    buffer_offsets(off_a, m0, p.M, p.K, wave, lane);
+    buffer_offsets(off_b, n0, p.N, p.K, wave, lane);
+    const uint32_t lds_base = lds_addr(smem) + wave * 8 * 1024;
     // Blocks of this wave inside the matrix: imax weight blocks (N % 128 == 0,
     // so 0 or 4), jmax activation blocks of 32 rows. Wave-uniform.
     const int64_t rows_w = p.M - (m0 + wm * 128), cols_w = p.N - (n0 + wn * 128);
@@ -575,55 +547,123 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    auto issue = [&](int s) {
-        const uint32_t st = lds_base + (s % P_STAGES) * P_STAGE;
-        const int64_t k0 = (int64_t)s * P_BK;
+    // Buffers of step s: A in (2 s) % 5, B in (2 s + 1) % 5.
+    auto a_buf = [&](int s) { return smem + ((2 * s) % R_BUFS) * R_BUF; };
+    auto b_buf = [&](int s) { return smem + ((2 * s + 1) % R_BUFS) * R_BUF; };
+    auto issue_a = [&](int s) {
+        const uint32_t dst = lds_base + ((2 * s) % R_BUFS) * R_BUF;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dma_16B_sbase(a_tile + k0, off_a[q], st + q * 1024);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) dma_16B_sbase(b_tile + k0, off_b[q], st + P_TILE + q * 1024);
+        for (int q = 0; q < 8; ++q) dma_16B_sbase(a_tile + (int64_t)s * BK, off_a[q], dst + q * 1024);
     };
-    const int pre = KT < P_STAGES - 1 ? KT : P_STAGES - 1;
-    for (int s = 0; s < pre; ++s) issue(s);
-    wait_stages_in_flight(pre - 1);
+    auto issue_b = [&](int s) {
+        const uint32_t dst = lds_base + ((2 * s + 1) % R_BUFS) * R_BUF;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma_16B_sbase(b_tile + (int64_t)s * BK, off_b[q], dst + q * 1024);
+    };
+    // Prologue: L(0) .. L(4), then wait for step 0 (L(0), L(1)).
+    issue_a(0);
+    issue_b(0);
+    if (KT > 1) {
+        issue_a(1);
+        issue_b(1);
+        if (KT > 2) {
+            issue_a(2);
+            asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        }
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();
 
     // The K loop, instantiated for whole tiles and for edge tiles (blocks
     // outside the matrix skipped); the choice is made once per tile.
     auto kloop = [&](auto edge_tag) {
         constexpr bool EDGE = decltype(edge_tag)::value;
-        // One K step on fragments `cur`, prefetching the next step into `nxt`.
-        auto step = [&](int kt, Frags& cur, Frags& nxt) {
-            // Stage kt+4 reuses the buffer of stage kt-1, which every wave
-            // finished reading before the previous step's barrier.
-            if (kt + P_STAGES - 1 < KT) issue(kt + P_STAGES - 1);
-            if (EDGE) mfma_half_partial<0>(acc, cur, imax, jmax);
-            else mfma_half<0>(acc, cur);
-            if (kt + 1 < KT) {
-                const int last = kt + P_STAGES - 1 < KT ? kt + P_STAGES - 1 : KT - 1;
-                wait_stages_in_flight(last - (kt + 1));  // stage kt+1 landed (this wave's part)
-                __syncthreads();                          // ... and every wave's part
-                read_pfrags(nxt, smem + ((kt + 1) % P_STAGES) * P_STAGE, wm, wn, lane);
-            }
+        Frags cur, nxt;
+        auto mfmas = [&](const Frags& f) {
             if (EDGE) {
-                mfma_half_partial<2>(acc, cur, imax, jmax);
+                mfma_slice_partial(acc, f, imax, jmax);
             } else {
-                mfma_half<2>(acc, cur);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two DS reads
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                }
+                mfma_slice(acc, f);
+                interleave_reads_with_mfma();
             }
         };
-        Frags f0, f1;
-        read_pfrags(f0, smem, wm, wn, lane);
-        int kt = 0;
-        for (; kt + 1 < KT; kt += 2) {
-            step(kt, f0, f1);
-            step(kt + 1, f1, f0);
+        // half 0 of step k: MFMAs on slice (k, 0), reads of slice (k, 1)
+        auto half0 = [&](int k) {
+            read_slice(nxt, a_buf(k), b_buf(k), 1, wm, wn, lane);
+            mfmas(cur);
+        };
+        // half 1 of step k: MFMAs on slice (k, 1), reads of slice (k + 1, 0)
+        auto half1 = [&](int k) {
+            read_slice(cur, a_buf(k + 1), b_buf(k + 1), 0, wm, wn, lane);
+            mfmas(nxt);
+        };
+        read_slice(cur, a_buf(0), b_buf(0), 0, wm, wn, lane);
+        int k = 0;
+        // Steady state: at the mid-step wait, A(k + 2) is still in flight.
+        // Half 1 of a steady-state step with the step's 16 DMA issues spread
+        // one per MFMA: a DMA issue stalls the wave while the address unit
+        // takes its 1 KB, and back to back after the barrier the 16 of them
+        // kept the matrix core idle for about 1000 cycles per step. Slot s
+        // holds one fragment read of slice (k + 1, 0) (s < 8), MFMA s on slice
+        // (k, 1) and DMA s (B(k + 2) regions, then A(k + 3) regions); the
+        // sched_barrier keeps each slot's instructions together.
+        auto half1_dma = [&](int k, auto with_a_tag) {
+            constexpr bool WITH_A = decltype(with_a_tag)::value;
+            const uint8_t* an = a_buf(k + 1);
+            const uint8_t* bn = b_buf(k + 1);
+            const uint32_t db = lds_base + ((2 * (k + 2) + 1) % R_BUFS) * R_BUF;
+            const uint32_t da = lds_base + ((2 * (k + 3)) % R_BUFS) * R_BUF;
+            const uint8_t* bsrc = b_tile + (int64_t)(k + 2) * BK;
+            const uint8_t* asrc = a_tile + (int64_t)(k + 3) * BK;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                if (s < 4) cur.b[s] = read_frag(bn, wn * 128 + s * 32 + (lane & 31), 0, lane);
+                else if (s < 8) cur.a[s - 4] = read_frag(an, wm * 128 + (s - 4) * 32 + (lane & 31), 0, lane);
+                acc[s >> 2][s & 3] = mfma(nxt.b[s >> 2], nxt.a[s & 3], acc[s >> 2][s & 3]);
+                if (s < 8) dma_16B_sbase(bsrc, off_b[s], db + s * 1024);
+                else if (WITH_A) dma_16B_sbase(asrc, off_a[s - 8], da + (s - 8) * 1024);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if constexpr (!EDGE) {
+            for (; k + 3 < KT; ++k) {
+                half0(k);
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // step k + 1 landed (this wave)
+                __syncthreads();                                  // ... every wave; step k's buffers free
+                half1_dma(k, std::true_type{});
+            }
+            if (k + 2 < KT) {
+                half0(k);
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+                __syncthreads();
+                half1_dma(k, std::false_type{});
+                ++k;
+            }
+        } else {
+            for (; k + 2 < KT; ++k) {
+                half0(k);
+                asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // step k + 1 landed (this wave)
+                __syncthreads();                                  // ... every wave; step k's buffers free
+                issue_b(k + 2);
+                if (k + 3 < KT) issue_a(k + 3);
+                half1(k);
+            }
         }
-        if (kt < KT) step(kt, f0, f1);
+        if (k + 1 < KT) {  // k = KT - 2: nothing left to issue
+            half0(k);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            half1(k);
+            ++k;
+        }
+        // k = KT - 1: the last slice's MFMAs read nothing further.
+        read_slice(nxt, a_buf(k), b_buf(k), 1, wm, wn, lane);
+        mfmas(cur);
+        if (EDGE) mfma_slice_partial(acc, nxt, imax, jmax);
+        else mfma_slice(acc, nxt);
     };
     if (whole) kloop(std::false_type{});
     else kloop(std::true_type{});
