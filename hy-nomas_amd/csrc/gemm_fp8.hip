@@ -670,6 +670,500 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
     epilogue<ROWCOL>(acc, p, m0, n0, smem, wave, wm, wn, lane, imax, jmax);
 }
 
+// ===========================================================================
+// Overlapped-epilogue row/column kernel (K >= 11 x 128): persistent, one
+// workgroup per CU walking its XCD's tile queue (tile_of order).
+//
+// With one wave per SIMD holding a 128 x 128 accumulator, an epilogue's VALU
+// work cannot overlap another wave's MFMAs -- only the same wave's. So the
+// wave carries each finished tile's output into the next tile's K loop:
+//   * after a tile's K loop it converts the accumulator to y = bf16(acc * sa *
+//     sb + bias) (128 VGPRs of packed pairs; the reference's linear output,
+//     rounded to bf16 before the activation as in the reference);
+//   * during the next tile's first nine K steps it applies the activation to
+//     y and writes it out through a 4 KB LDS staging area -- eight passes of
+//     32 rows x 64 columns, one per step, one element per MFMA slot, with the
+//     128-byte row read-back and the stores of pass p in step p + 1.
+// Registers: fragments are read "rolling" into the registers their last MFMA
+// of the slice has just read (slot s = 4 i + j runs MFMA (i, j); B block i is
+// replaced after slot 4 i + 3, A block j after slot 12 + j), 64 VGPRs instead
+// of 128. LDS: four 32 KB stage buffers (two K steps: step s in pair (s + par)
+// & 1), the staging areas and the epilogue parameters (DMA'd in step 0).
+//
+// Step k: half 0 -- MFMAs of slice (k, 0), reads of slice (k, 1); wait for
+// step k + 1 (vmcnt(0)) and barrier; half 1 -- MFMAs of slice (k, 1), reads of
+// slice (k + 1, 0), and the 16 DMAs of step k + 2 into step k's pair (one per
+// slot). Step KT - 2 loads the next tile's step 0 instead, and after the last
+// step the next tile's step 1 goes into the last pair: the next tile's first
+// wait finds its data landed. Stores issued in a half 1 are drained by the
+// following mid-step wait; every load wait is either vmcnt(0) or a count that
+// a pending wanted load cannot satisfy (loads complete in order among
+// themselves).
+constexpr int O_BUFS = 4;
+constexpr int O_STAGE = 32 * 128;                   // per wave: 32 rows x 64 bf16
+constexpr int O_PARAMS = 1280;                      // per wave: 128 + 128 floats, 128 bf16
+constexpr int O_STAGE_BASE = O_BUFS * R_BUF;
+constexpr int O_PARAM_BASE = O_STAGE_BASE + 4 * O_STAGE;
+constexpr int O_SMEM = O_PARAM_BASE + 4 * O_PARAMS;
+constexpr int O_JO = 2;                             // row blocks carried into the next tile
+constexpr int O_PASSES = 2 * O_JO;                  // overlapped passes (steps 0 .. O_PASSES - 1)
+constexpr int O_MIN_KT = O_PASSES + 3;              // + the tail step + the last two steps
+static_assert(O_SMEM <= 160 * 1024, "LDS");
+
+// The lane id, regenerated in place (v_mbcnt) by a volatile asm: values
+// derived from it are recomputed where used rather than hoisted and held live
+// across the tile loop.
+HN_DEVICE int fresh_lane() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+HN_DEVICE void dma_4B_sbase(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %0, %1"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds)
+        : "memory", "m0");
+}
+
+// Parameter DMA q (0..4) of a wave's sub-tile, 256 bytes each: row scales at
+// [0, 512), column scales at [512, 1024), bias pairs at [1024, 1280). Indices
+// are clamped to the operand's end (in bounds; never used).
+HN_DEVICE void param_dma(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane, uint32_t lds, int q) {
+    if (q < 2) {
+        int64_t m = m0 + wm * 128 + 64 * q + lane;
+        m = m < p.M ? m : p.M - 1;
+        dma_4B_sbase(p.sa, (uint32_t)(m * 4), lds + 256 * q);
+    } else if (q < 4) {
+        int64_t n = n0 + wn * 128 + 64 * (q - 2) + lane;
+        n = n < p.N ? n : p.N - 1;
+        dma_4B_sbase(p.sb, (uint32_t)(n * 4), lds + 512 + 256 * (q - 2));
+    } else if (p.bias) {
+        int64_t n = n0 + wn * 128 + 2 * lane;
+        n = n < p.N ? n : p.N - 2;
+        dma_4B_sbase(p.bias, (uint32_t)(n * 2), lds + 1024);
+    } else {
+        // No bias: zeros, so the conversion reads the area unconditionally.
+        __attribute__((address_space(3))) uint32_t* z =
+            (__attribute__((address_space(3))) uint32_t*)(uintptr_t)(lds + 1024);
+        z[lane] = 0u;
+    }
+}
+
+// y[i][j][w] (j < O_JO) = bf16 pair (2 w, 2 w + 1) of block (i, j): columns
+// 32 i + 8 (w / 2) + 4 (lane / 32) + 2 (w % 2) + {0, 1}, row 32 j + lane % 32
+// of the sub-tile.
+// Column groups outer, row blocks inner: one group's scales and bias live at a
+// time. The bias area holds zeros when the layer has no bias.
+HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], const uint8_t* prm, int lane) {
+    const float* const psa = reinterpret_cast<const float*>(prm);
+    const float* const psb = reinterpret_cast<const float*>(prm + 512);
+    const uint16_t* const pbias = reinterpret_cast<const uint16_t*>(prm + 1024);
+    const int h = lane >> 5, r = lane & 31;
+    float sam[O_JO];
+#pragma unroll
+    for (int j = 0; j < O_JO; ++j) sam[j] = psa[32 * j + r];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+            const int nl = 32 * i + 8 * vq + 4 * h;
+            const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
+            const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
+            const float bn0 = bf16_bits_to_f32(bb.x & 0xffffu), bn1 = bf16_bits_to_f32(bb.x >> 16);
+            const float bn2 = bf16_bits_to_f32(bb.y & 0xffffu), bn3 = bf16_bits_to_f32(bb.y >> 16);
+#pragma unroll
+            for (int j = 0; j < O_JO; ++j) {
+                const float y0 = fmaf(acc[i][j][4 * vq + 0], sam[j] * sb4.x, bn0);
+                const float y1 = fmaf(acc[i][j][4 * vq + 1], sam[j] * sb4.y, bn1);
+                const float y2 = fmaf(acc[i][j][4 * vq + 2], sam[j] * sb4.z, bn2);
+                const float y3 = fmaf(acc[i][j][4 * vq + 3], sam[j] * sb4.w, bn3);
+                y[i][j][2 * vq] = pack_bf16(y0, y1);
+                y[i][j][2 * vq + 1] = pack_bf16(y2, y3);
+            }
+        }
+}
+
+// Pass P (block row j = P / 2, weight blocks 2 (P % 2) + {0, 1}) covers the
+// 32 carried values x = 16 ii + 4 vq + e of a lane; group g = x / 4 holds 4
+// consecutive columns (one 8-byte staging write; 128-byte staging rows with
+// 16-byte chunk c at position c ^ ((r >> 1) & 7)).
+//
+// oe_act: the activation of value x in place (bf16 in, bf16 out; the even
+// value of a pair is held in glo until the odd one repacks the word).
+template <int ACT>
+HN_DEVICE void oe_act(uint32_t (&y)[4][4][8], float& glo, int P, int x) {
+    if (ACT != HN_ACT_GELU_TANH) return;
+    const int j = P >> 1, i = 2 * (P & 1) + (x >> 4), vq = (x >> 2) & 3, e = x & 3;
+    uint32_t& w = y[i][j][2 * vq + (e >> 1)];
+    if ((e & 1) == 0) glo = gelu_tanh(__uint_as_float(w << 16));
+    else w = pack_bf16(glo, gelu_tanh(__uint_as_float(w & 0xffff0000u)));
+}
+
+HN_DEVICE void oe_write(const uint32_t (&y)[4][4][8], uint8_t* stg, int P, int g, int lane) {
+    const int j = P >> 1, ii = g >> 2, vq = g & 3, i = 2 * (P & 1) + ii;
+    const int r = lane & 31, h = lane >> 5, c = 4 * ii + vq;
+    *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * h) =
+        make_uint2(y[i][j][2 * vq], y[i][j][2 * vq + 1]);
+}
+
+// Staging read-back q (0..3) of a pass: rows 8 q + lane / 8, 16-byte chunk lane % 8.
+HN_DEVICE uint4 oe_readback(const uint8_t* stg, int q, int lane) {
+    const int rr = 8 * q + (lane >> 3), c = lane & 7;
+    return *reinterpret_cast<const uint4*>(stg + rr * 128 + ((c ^ ((rr >> 1) & 7)) << 4));
+}
+
+HN_DEVICE void oe_store(const Params& p, int64_t pm0, int64_t pn0, int wm, int wn, int P, int q, const uint4& v,
+                        int lane) {
+    const int j = P >> 1, ih = P & 1;
+    const int rr = 8 * q + (lane >> 3), c = lane & 7;
+    const int64_t m = pm0 + wm * 128 + 32 * j + rr;
+    const int64_t n = pn0 + wn * 128 + 64 * ih + 8 * c;
+    if (m < p.M && n < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) = v;
+}
+
+// All eight passes of a pending tile without overlap (before an edge tile and
+// after a workgroup's last tile).
+template <int ACT>
+HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, int64_t pm0, int64_t pn0,
+                        int wm, int wn, int lane) {
+#pragma unroll
+    for (int P = 0; P < O_PASSES; ++P) {
+        float glo = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 32; ++x) oe_act<ACT>(y, glo, P, x);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) oe_write(y, stg, P, g, lane);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) oe_store(p, pm0, pn0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
+    }
+}
+
+// Passes 2 j, 2 j + 1 for the row blocks j >= O_JO straight from the
+// accumulator (not carried): scale, bias, activation, staging, stores.
+template <int ACT>
+HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, uint8_t* stg, int64_t m0,
+                             int64_t n0, int wm, int wn, int lane) {
+    const int h = lane >> 5, r = lane & 31;
+#pragma unroll
+    for (int P = O_PASSES; P < 8; ++P) {
+        // Parameters re-read per pass (opaque offset): common loads kept
+        // across the passes would hold 32 column-scale vectors live.
+        int z = 0;
+        asm volatile("" : "+s"(z));
+        const float* const psa = reinterpret_cast<const float*>(prm + z);
+        const float* const psb = reinterpret_cast<const float*>(prm + z + 512);
+        const uint16_t* const pbias = reinterpret_cast<const uint16_t*>(prm + z + 1024);
+        const int j = P >> 1, ih = P & 1;
+        const float sam = psa[32 * j + r];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int i = 2 * ih + ii, nl = 32 * i + 8 * vq + 4 * h;
+                const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
+                const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
+                float v[4] = {fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bf16_bits_to_f32(bb.x & 0xffffu)),
+                              fmaf(acc[i][j][4 * vq + 1], sam * sb4.y, bf16_bits_to_f32(bb.x >> 16)),
+                              fmaf(acc[i][j][4 * vq + 2], sam * sb4.z, bf16_bits_to_f32(bb.y & 0xffffu)),
+                              fmaf(acc[i][j][4 * vq + 3], sam * sb4.w, bf16_bits_to_f32(bb.y >> 16))};
+                // The activation sees the bf16-rounded linear output, as when carried.
+                uint2 o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                if (ACT == HN_ACT_GELU_TANH) {
+                    v[0] = gelu_tanh(__uint_as_float(o.x << 16));
+                    v[1] = gelu_tanh(__uint_as_float(o.x & 0xffff0000u));
+                    v[2] = gelu_tanh(__uint_as_float(o.y << 16));
+                    v[3] = gelu_tanh(__uint_as_float(o.y & 0xffff0000u));
+                    o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+                }
+                const int c = 4 * ii + vq;
+                *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * h) = o;
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) oe_store(p, m0, n0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
+    }
+}
+
+template <int ACT>
+__global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[O_SMEM];
+    const int xcd = blockIdx.x & 7;
+    const int stride = (int)(gridDim.x >> 3);  // workgroups per XCD
+    int slot = (int)(blockIdx.x >> 3);
+    int tm, tn;
+    if (!tile_of(p, xcd + 8 * slot, tm, tn)) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int KT = (int)(p.K / BK);
+    const uint32_t lds_base = lds_addr(smem) + wave * 8 * 1024;
+    uint8_t* const stg = smem + O_STAGE_BASE + wave * O_STAGE;
+    const uint8_t* const prm = smem + O_PARAM_BASE + wave * O_PARAMS;
+    const uint32_t prm_lds = lds_addr(prm);
+
+    // DMA source: the tile whose stages are being loaded. A 1 KB load q of
+    // a buffer fills rows 8 (8 wave + q) .. + 7 (lane / 8 each) with the
+    // swizzled logical chunk of physical chunk lane % 8; its per-lane offset
+    // is computed at issue from the lane's row (lrow + 8 q, clamped to the
+    // operand's last row: in bounds, never stored) and chunk offset, which
+    // depends only on q % 2 (chunk[q & 1]).
+    const uint8_t* a_src = nullptr;
+    const uint8_t* b_src = nullptr;
+    int a_last = 0, b_last = 0;  // last valid row of the source tile, tile-relative
+    auto set_src = [&](int tm_, int tn_) {
+        const int64_t m0_ = (int64_t)tm_ * BM, n0_ = (int64_t)tn_ * BN;
+        a_src = p.a + m0_ * p.K;
+        b_src = p.b + n0_ * p.K;
+        a_last = (int)((p.M - m0_ < BM ? p.M - m0_ : BM) - 1);
+        b_last = (int)((p.N - n0_ < BN ? p.N - n0_ : BN) - 1);
+    };
+    // Per-lane DMA geometry from a regenerated lane id l: the lane's row in
+    // load 0 and its chunk offsets for even and odd loads.
+    struct DmaLane {
+        int row;
+        uint32_t chunk[2];
+    };
+    auto dma_lane = [&](int l) {
+        DmaLane d;
+        d.row = wave * 64 + (l >> 3);
+        d.chunk[0] = (uint32_t)swz_pos(d.row, l & 7) << 4;
+        d.chunk[1] = (uint32_t)swz_pos(d.row + 8, l & 7) << 4;
+        return d;
+    };
+    auto dma_off = [&](const DmaLane& d, int q, int last) {
+        const int row = min(d.row + 8 * q, last);
+        return (uint32_t)row * (uint32_t)p.K + d.chunk[q & 1];
+    };
+    // Current tile: origin and blocks inside the matrix (imax weight blocks,
+    // 0 or 4 as N % 128 == 0; jmax activation blocks of 32 rows). Wave-uniform.
+    int64_t cm0 = 0, cn0 = 0;
+    int cimax = 0, cjmax = 0;
+    auto set_cur = [&](int tm_, int tn_) {
+        cm0 = (int64_t)tm_ * BM;
+        cn0 = (int64_t)tn_ * BN;
+        const int64_t rows_w = p.M - (cm0 + wm * 128), cols_w = p.N - (cn0 + wn * 128);
+        cjmax = rows_w >= 128 ? 4 : (rows_w <= 0 ? 0 : (int)((rows_w + 31) >> 5));
+        cimax = cols_w >= 128 ? 4 : (cols_w <= 0 ? 0 : (int)(cols_w >> 5));
+    };
+    int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
+    auto pair_of = [&](int s) { return (s + par) & 1; };
+    auto dma_a = [&](const DmaLane& d, int src_step, int pr, int q) {
+        dma_16B_sbase(a_src + (int64_t)src_step * BK, dma_off(d, q, a_last), lds_base + (2 * pr) * R_BUF + q * 1024);
+    };
+    auto dma_b = [&](const DmaLane& d, int src_step, int pr, int q) {
+        dma_16B_sbase(b_src + (int64_t)src_step * BK, dma_off(d, q, b_last),
+                      lds_base + (2 * pr + 1) * R_BUF + q * 1024);
+    };
+
+    f32x16 acc[4][4];
+    i32x8 fa[4], fb[4];
+    uint32_t y[4][4][8];         // carried rows (j < O_JO) of the pending tile
+    int64_t pm0 = p.M, pn0 = 0;  // pending tile origin (none yet: every store out of range)
+    bool pending = false;
+
+    // Fragment reads. A fragment of block row base + 32 q is 16-byte chunks
+    // c0 = 4 kh + 2 (lane / 32) and c0 + 1 of row base + 32 q + lane % 32; the
+    // swizzle depends only on the lane (32 q and base are multiples of 16), so
+    // a lane needs four offsets (kh x chunk), computed per step from a
+    // regenerated lane id (hoisted, they would be held live and spilled).
+    struct RdLane {
+        uint32_t off[2][2];
+    };
+    auto rd_lane = [&](int l) {
+        RdLane d;
+        const int r = l & 31, c0 = (l >> 5) * 2;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi)
+                d.off[kh][hi] = (uint32_t)(r * BK + (swz_pos(r, 4 * kh + c0 + hi) << 4));
+        return d;
+    };
+    auto frag_at = [&](const uint8_t* buf, int row0, int kh, const RdLane& d) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(buf + row0 * BK + d.off[kh][0]);
+        const uint4 hi = *reinterpret_cast<const uint4*>(buf + row0 * BK + d.off[kh][1]);
+        i32x8 f;
+        f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+        f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+        return f;
+    };
+    auto read_a = [&](const uint8_t* buf, int j, int kh, const RdLane& d) {
+        fa[j] = frag_at(buf, wm * 128 + j * 32, kh, d);
+    };
+    auto read_b = [&](const uint8_t* buf, int i, int kh, const RdLane& d) {
+        fb[i] = frag_at(buf, wn * 128 + i * 32, kh, d);
+    };
+    // Rolling reads of the next slice after slot s's MFMA.
+    auto roll = [&](int s, const uint8_t* abuf, const uint8_t* bbuf, int kh, const RdLane& d) {
+        if (s == 3 || s == 7 || s == 11) read_b(bbuf, s >> 2, kh, d);
+        if (s >= 12) read_a(abuf, s - 12, kh, d);
+        if (s == 15) read_b(bbuf, 3, kh, d);
+    };
+
+    // One K step. EDGE: edge tile (blocks outside the matrix skipped). PASS:
+    // -1 none, 0 .. O_PASSES - 1 epilogue pass of the pending tile (plus the
+    // read-back and stores of pass PASS - 1), O_PASSES only the read-back and
+    // stores of the last pass.
+    // DMA: 0 none, 1 this tile's step k + 2, 2 the next tile's step 0, 3 as 1
+    // plus this tile's epilogue parameters. NEXT: reads of slice (k + 1, 0)
+    // and the mid-step wait (false on the last step). FIRST: the accumulator
+    // starts at zero (step 0).
+    auto step = [&](int k, auto edge_t, auto pass_t, auto dma_t, auto next_t, auto first_t) {
+        constexpr bool EDGE = decltype(edge_t)::value;
+        constexpr int PASS = decltype(pass_t)::value;
+        constexpr int DMA = decltype(dma_t)::value;
+        constexpr bool NEXT = decltype(next_t)::value;
+        constexpr bool FIRST = decltype(first_t)::value;
+        const uint8_t* const ab = smem + (2 * pair_of(k)) * R_BUF;
+        const uint8_t* const bb = ab + R_BUF;
+        const uint8_t* const an = smem + (2 * pair_of(k + 1)) * R_BUF;
+        const uint8_t* const bnx = an + R_BUF;
+        const int dst = pair_of(k);
+        float glo = 0.0f;
+        uint4 rb[4];
+        const int el = fresh_lane();
+        const DmaLane dl = dma_lane(el);
+        const RdLane rl = rd_lane(el);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int i = s >> 2, j = s & 3;
+            if (!EDGE || (i < cimax && j < cjmax)) {
+                if (FIRST) acc[i][j] = mfma(fb[i], fa[j], f32x16{});
+                else acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
+            } else if (FIRST) {
+                acc[i][j] = f32x16{};
+            }
+            roll(s, ab, bb, 1, rl);
+            if (PASS >= 0 && PASS < O_PASSES) oe_act<ACT>(y, glo, PASS, s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (NEXT) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // step k + 1 landed (this wave)
+            __syncthreads();                                  // ... every wave; step k's pair free
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            // Read-back of the previous pass (slots 0-3) before this pass's
+            // staging writes (slots 3-15), stores two slots after each read.
+            if (PASS >= 1 && s < 4) rb[s] = oe_readback(stg, s, el);
+            if (PASS >= 1 && s >= 2 && s < 6) oe_store(p, pm0, pn0, wm, wn, PASS - 1, s - 2, rb[s - 2], el);
+            const int i = s >> 2, j = s & 3;
+            if (!EDGE || (i < cimax && j < cjmax)) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
+            if (NEXT) roll(s, an, bnx, 0, rl);
+            if (DMA == 1 || DMA == 3) {
+                if (s < 8) dma_a(dl, k + 2, dst, s);
+                else dma_b(dl, k + 2, dst, s - 8);
+            }
+            if (DMA == 2) {
+                if (s < 8) dma_a(dl, 0, dst, s);
+                else dma_b(dl, 0, dst, s - 8);
+            }
+            if (DMA == 3 && s >= 8 && s < 13) param_dma(p, cm0, cn0, wm, wn, el, prm_lds, s - 8);
+            if (PASS >= 0 && PASS < O_PASSES) {
+                oe_act<ACT>(y, glo, PASS, 16 + s);
+                if (s >= 4 && s < 8) oe_write(y, stg, PASS, s - 4, el);         // groups 0-3 (half 0)
+                if ((s & 3) == 3) oe_write(y, stg, PASS, 4 + (s >> 2), el);     // groups 4-7, when complete
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using F = std::false_type;
+    using T = std::true_type;
+
+    // First tile: steps 0 and 1 into pairs 0 and 1.
+    set_src(tm, tn);
+    set_cur(tm, tn);
+    {
+        const DmaLane d = dma_lane(fresh_lane());
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma_a(d, 0, 0, q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma_b(d, 0, 0, q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma_a(d, 1, 1, q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma_b(d, 1, 1, q);
+    }
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // step 0: step 1's 16 loads are newer
+    __syncthreads();
+
+    for (;;) {
+        int ntm = 0, ntn = 0;
+        const bool more = tile_of(p, xcd + 8 * (slot + stride), ntm, ntn);
+        // Slice (0, 0).
+        {
+            const uint8_t* const ab = smem + (2 * pair_of(0)) * R_BUF;
+            const RdLane d = rd_lane(fresh_lane());
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                read_b(ab + R_BUF, q, 0, d);
+                read_a(ab, q, 0, d);
+            }
+        }
+        const bool whole = cimax == 4 && cjmax == 4;
+        if (whole) {
+            if (!pending) {
+                // Nothing carried yet: the passes run on zeros, their stores
+                // all out of range.
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < O_JO; ++j)
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) y[i][j][w] = 0u;
+            }
+            step(0, F{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{}, T{}, T{});
+            step(1, F{}, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            step(2, F{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            step(3, F{}, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            step(4, F{}, std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            static_assert(O_PASSES == 4, "the unrolled epilogue steps assume four passes");
+            for (int k = O_PASSES + 1; k < KT - 2; ++k)
+                step(k, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            if (more) set_src(ntm, ntn);  // else step 0 of this tile again: harmless, in bounds
+            step(KT - 2, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 2>{}, T{}, F{});
+            step(KT - 1, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 0>{}, F{}, F{});
+        } else {
+            if (pending) oe_flush<ACT>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+            step(0, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 3>{}, T{}, T{});
+            for (int k = 1; k < KT - 2; ++k)
+                step(k, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            if (more) set_src(ntm, ntn);
+            step(KT - 2, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 2>{}, T{}, F{});
+            step(KT - 1, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 0>{}, F{}, F{});
+        }
+        // Every wave is done reading the last step's pair.
+        __syncthreads();
+        if (more) {
+            // The next tile's step 1 into the last step's pair.
+            const int pr = pair_of(KT - 1);
+            const DmaLane d = dma_lane(fresh_lane());
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dma_a(d, 1, pr, q);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
+        }
+        direct_passes<ACT>(p, acc, prm, stg, cm0, cn0, wm, wn, fresh_lane());
+        convert_tile(acc, y, prm, fresh_lane());
+        pm0 = cm0;
+        pn0 = cn0;
+        pending = true;
+        if (!more) break;
+        par = (KT + par) & 1;
+        set_cur(ntm, ntn);
+        slot += stride;
+        // The next tile's step 0 landed: step 1's 16 loads are newer.
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        __syncthreads();
+    }
+    oe_flush<ACT>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+    // The last step's re-load of step 0 (no next tile) may still be landing.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 }  // namespace gemm
 }  // namespace hn
 
@@ -705,7 +1199,15 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     p.tiles_part = (int)(tm * tn) - p.tiles_full;
     if (mode == gemm::ROWCOL) p.per_xcd = (p.tiles_full + 7) / 8 + (p.tiles_part + 7) / 8;
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    if (mode == gemm::ROWCOL)
+    if (mode == gemm::ROWCOL && K / gemm::BK >= gemm::O_MIN_KT) {
+        // Persistent: per XCD, min(queue length, CUs of the XCD) workgroups.
+        const int per_xcd_cus = device_cus() / 8 > 0 ? device_cus() / 8 : 1;
+        const dim3 pgrid((unsigned)(8 * (p.per_xcd < per_xcd_cus ? p.per_xcd : per_xcd_cus)));
+        if (act == HN_ACT_GELU_TANH)
+            gemm::gemm_rowcol_oe_kernel<HN_ACT_GELU_TANH><<<pgrid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+        else
+            gemm::gemm_rowcol_oe_kernel<HN_ACT_NONE><<<pgrid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+    } else if (mode == gemm::ROWCOL)
         gemm::gemm_rowcol_kernel<<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     else
         gemm::gemm_fp8_kernel<gemm::BLOCKWISE><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);

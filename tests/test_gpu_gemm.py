@@ -82,6 +82,40 @@ def test_linear_fp8_no_bias_and_strided_out(O, dev):
     assert (out[:, 128:] == 3.0).all()
 
 
+# K >= 7 x 128 takes the persistent kernel that carries half of each tile's
+# epilogue into the next tile's K loop. Cases: the smallest such K and the
+# largest K below it; ragged M and N (edge tiles); more tiles than CUs, so a
+# workgroup walks whole and edge tiles in turn; with and without bias / GELU.
+@pytest.mark.parametrize("M,K,N,gelu,bias", [
+    (300, 896, 384, True, True),      # smallest K on the carried-epilogue path
+    (300, 768, 384, True, True),      # largest K below it
+    (1000, 1280, 640, True, True),    # M and N edges, 12 tiles
+    (4700, 1024, 4224, True, False),  # 323 tiles: two per workgroup, both edges, no bias
+    (4700, 1024, 4224, False, True),
+])
+def test_linear_fp8_persistent_tiles(O, dev, M, K, N, gelu, bias):
+    print(f"case linear persistent {M}x{K}x{N} gelu={gelu} bias={bias}", flush=True)
+    rows = None if M <= 1000 else np.concatenate([np.arange(0, 64), np.arange(2300, 2364), np.arange(4400, 4700)])
+    _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
+
+
+def test_gemm_rowcol_persistent_strided_out(dev):
+    """ldc > N on the carried-epilogue path (K = 1024): columns past N untouched."""
+    ops = pkg_module("ops")
+    L = pkg_module("_lib")
+    a = torch.randint(0, 120, (300, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (384, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    sa = torch.rand(300, device=dev) + 0.5
+    sb = torch.rand(384, device=dev) + 0.5
+    out = torch.full((300, 392), 3.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.load().hn_gemm_fp8_rowcol(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+                                        None, out.data_ptr(), 300, 384, 1024, 392, 0,
+                                        torch.cuda.current_stream().cuda_stream), "gemm")
+    ref = ops.gemm_fp8_rowcol(a, b, sa, sb)
+    assert torch.equal(out[:, :384], ref)
+    assert (out[:, 384:] == 3.0).all()
+
+
 def test_gemm_rowcol_is_deterministic(dev):
     ops = pkg_module("ops")
     a = torch.randint(0, 120, (1000, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
