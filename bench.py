@@ -76,8 +76,12 @@ def time_loop(fn, steps, warmup, stream=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 100 timed steps after 50 warmup steps: the north-star linear is ~0.4 ms,
+    # and 20 steps after 5 warmup fell inside the clock transient of a GPU
+    # coming out of idle (the same GEMM's calls drift from 410 to 510 us and
+    # back within the first ~30 calls), reading 15 % low.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
