@@ -32,6 +32,7 @@ SIGNATURES = {
     "hn_abi_version": [],
     "hn_quantize_rows_fp8": [_P, _I64, _I64, _I64, _I, _F, _P, _P, _P],
     "hn_quantize_blockwise_fp8": [_P, _I64, _I64, _P, _P, _P],
+    "hn_ln_mod_quantize_fp8": [_P, _I64, _I64, _I64, _P, _P, _I64, _F, _F, _P, _P, _P],
     "hn_kv_quantize": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _PI64, _P, _PI64, _I64, _P],
     "hn_kv_quantize_pair": [_I, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P,
                             _PI64, _I64, _P],

@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 #define HN_DEVICE __device__ __forceinline__
 
@@ -27,6 +28,18 @@ HN_DEVICE uint32_t f32_to_bf16_bits(float f) {
     u += 0x7fffu + ((u >> 16) & 1u);
     return u >> 16;
 }
+
+// Two fp32 -> one word of two bf16 (lo in bits 0-15), one v_cvt_pk_bf16_f32.
+// Round to nearest even: equal to f32_to_bf16_bits for every finite fp32
+// (all 2^32 patterns compared on gfx950); a NaN stays a NaN of its own sign.
+HN_DEVICE uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
+// The low / high bf16 of a word, as fp32 (exact).
+HN_DEVICE float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+HN_DEVICE float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // fp32 -> OCP e4m3 ("fn") byte, round to nearest even on the e4m3 grid.
 // The grid is extended one step past 448 (480, bit pattern 0x7F): values that
@@ -79,16 +92,28 @@ HN_DEVICE uint32_t e4m3_encode4(float a, float b, float c, float d) {
 // pairs per rule). The check holds for s >= 2^-100; smaller or non-finite
 // scales (rows whose amax is within ~2^-91 of zero, or non-finite rows) take
 // the IEEE division, since there the residual e underflows.
+//
+// `exact` is a property of the row, so callers choose the form once per row
+// (with_form) and instantiate their encode loop for each (at<EXACT>), instead
+// of a branch per element.
 struct Quot {
     float s, r;
     bool exact;
     HN_DEVICE explicit Quot(float scale)
         : s(scale), r(1.0f / scale), exact(!(scale >= 0x1p-100f && scale <= 3.4028234e38f)) {}
-    HN_DEVICE float operator()(float x) const {
-        if (exact) return x / s;
+    template <bool EXACT>
+    HN_DEVICE float at(float x) const {
+        if (EXACT) return x / s;
         const float y = __fmul_rn(x, r);
         const float e = __fmaf_rn(-s, y, x);
         return __builtin_copysignf(__fmaf_rn(e, r, y), x);
+    }
+    HN_DEVICE float operator()(float x) const { return exact ? at<true>(x) : at<false>(x); }
+    // f(std::integral_constant<bool, EXACT>) for this row's form
+    template <class F>
+    HN_DEVICE void with_form(F&& f) const {
+        if (exact) f(std::integral_constant<bool, true>{});
+        else f(std::integral_constant<bool, false>{});
     }
 };
 
@@ -98,6 +123,28 @@ HN_DEVICE uint32_t int8_code(float v) {
     float r = v >= 0.0f ? floorf(v + 0.5f) : ceilf(v - 0.5f);
     r = fminf(fmaxf(r, -127.0f), 127.0f);
     return (uint32_t)(int32_t)r & 0xffu;
+}
+
+// The 8 codes (e4m3 if FP8, else INT8) of one lane's 8 values of a row with
+// quotient d; the quotient form is chosen once for the 8.
+template <bool FP8>
+HN_DEVICE uint2 codes8(const float (&f)[8], const Quot& d) {
+    uint2 out;
+    d.with_form([&](auto form) {
+        constexpr bool E = decltype(form)::value;
+        if (FP8) {
+            out.x = e4m3_encode4(d.at<E>(f[0]), d.at<E>(f[1]), d.at<E>(f[2]), d.at<E>(f[3]));
+            out.y = e4m3_encode4(d.at<E>(f[4]), d.at<E>(f[5]), d.at<E>(f[6]), d.at<E>(f[7]));
+        } else {
+            out.x = out.y = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                out.x |= int8_code(d.at<E>(f[j])) << (8 * j);
+                out.y |= int8_code(d.at<E>(f[j + 4])) << (8 * j);
+            }
+        }
+    });
+    return out;
 }
 
 // OCP e4m3 byte -> fp32 (exact).

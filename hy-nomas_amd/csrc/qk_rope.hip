@@ -61,20 +61,25 @@ HN_DEVICE uint4 pack8(const float (&f)[8]) {
 HN_DEVICE float bf16_round(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
 
 // RMSNorm + RoPE of one row's 8 dims held by this lane (d0 = 8 * lane16).
+// Every fp32 operation rounds on its own, as the reference's tensor ops do:
+// contraction is off (the RoPE sum would otherwise fuse into an FMA) and the
+// square root is the correctly rounded sqrtf (__fsqrt_rn is the native
+// 1-ulp v_sqrt_f32).
 HN_DEVICE void norm_rope(float (&x)[8], const float (&w)[8], const float (&c)[8], const float (&s)[8],
                          float eps) {
+#pragma clang fp contract(off)
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fmul_rn(x[j], x[j]));
+    for (int j = 0; j < 8; ++j) ss = ss + x[j] * x[j];
     ss = group_sum<16>(ss);
-    const float r = 1.0f / __fsqrt_rn(__fadd_rn(ss * (1.0f / 128.0f), eps));
+    const float r = 1.0f / sqrtf(ss * (1.0f / 128.0f) + eps);
     float y[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = bf16_round(__fmul_rn(bf16_round(__fmul_rn(x[j], r)), w[j]));
+    for (int j = 0; j < 8; ++j) y[j] = bf16_round(bf16_round(x[j] * r) * w[j]);
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-        x[j] = __fadd_rn(__fmul_rn(y[j], c[j]), __fmul_rn(-y[j + 1], s[j]));
-        x[j + 1] = __fadd_rn(__fmul_rn(y[j + 1], c[j + 1]), __fmul_rn(y[j], s[j + 1]));
+        x[j] = y[j] * c[j] + (-y[j + 1]) * s[j];
+        x[j + 1] = y[j + 1] * c[j + 1] + y[j] * s[j + 1];
     }
 }
 
@@ -87,20 +92,7 @@ HN_DEVICE void quantize_row(const float (&f)[8], uint8_t* code_row, float* scale
     amax = group_max<16>(amax);
     const float qmax = FMT == HN_KV_FP8 ? kE4M3Max : 127.0f;
     const float s = amax > 0.0f ? amax / qmax : 1.0f;
-    const Quot d(s);
-    uint32_t lo, hi;
-    if (FMT == HN_KV_FP8) {
-        lo = e4m3_encode4(d(f[0]), d(f[1]), d(f[2]), d(f[3]));
-        hi = e4m3_encode4(d(f[4]), d(f[5]), d(f[6]), d(f[7]));
-    } else {
-        lo = hi = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            lo |= int8_code(d(f[j])) << (8 * j);
-            hi |= int8_code(d(f[j + 4])) << (8 * j);
-        }
-    }
-    *reinterpret_cast<uint2*>(code_row + lane16 * 8) = make_uint2(lo, hi);
+    *reinterpret_cast<uint2*>(code_row + lane16 * 8) = codes8<FMT == HN_KV_FP8>(f, Quot(s));
     if (lane16 == 0) *scale = s;
 }
 

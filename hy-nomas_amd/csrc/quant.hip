@@ -14,13 +14,14 @@ namespace hn {
 
 // Eight bf16 (one uint4) -> eight e4m3 codes of fl32(x / s), then RNE to
 // e4m3, as two dwords.
+template <bool EXACT>
 HN_DEVICE uint2 encode8(const uint4& v, const Quot& d) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     float f[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        f[2 * j] = d(bf16_bits_to_f32(w[j] & 0xffffu));
-        f[2 * j + 1] = d(bf16_bits_to_f32(w[j] >> 16));
+        f[2 * j] = d.at<EXACT>(bf16_lo(w[j]));
+        f[2 * j + 1] = d.at<EXACT>(bf16_hi(w[j]));
     }
     return make_uint2(e4m3_encode4(f[0], f[1], f[2], f[3]), e4m3_encode4(f[4], f[5], f[6], f[7]));
 }
@@ -64,11 +65,131 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     if (lane == 0) scale[row] = s;
     const Quot d(s);
     uint8_t* qr = q + row * cols;
+    d.with_form([&](auto form) {
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = lane + i * 64;
-        if (c < nchunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8(v[i], d);
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (c < nchunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8<decltype(form)::value>(v[i], d);
+        }
+    });
     }
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm (no affine) + adaLN modulate + per-token FP8 quantization, fused:
+//   y = bf16((x - mean) * rsqrt(var + eps))            F.layer_norm on bf16
+//   o = bf16(bf16(y * bf16(1 + scale[c])) + shift[c])  _modulate in bf16 ops
+//   per-token e4m3 codes of o with the quantize_rows_kernel recipe.
+// Each bf16 rounding is one of the reference's bf16 tensor ops
+// (nomas_compile_prepost.py:14-15,40-43,81-84), so only the fp32 mean and
+// variance differ from the unfused path (the order of their sums), which can
+// move a LayerNorm output by one bf16 ulp at a rounding boundary. The sums have
+// a fixed order and the kernel body turns FP contraction off (the compiler
+// would otherwise fuse ss + d * d into one FMA; HIP's __fmul_rn / __fadd_rn
+// are plain operators that keep the header's contraction setting, so the
+// body uses operators under the pragma); lane l adds its values in storage
+// order (chunks l, l + 64, ..., 8 values each),
+// then the lanes combine by xor butterfly (every lane ends with the same sum,
+// fp addition being commutative); mean = sum * (1 / cols), var = sum((x -
+// mean)^2) * (1 / cols), rstd = 1 / sqrt(var + eps), all fp32 and correctly
+// rounded (sqrtf, not __fsqrt_rn, which is the native 1-ulp v_sqrt_f32). One wave per row as in quantize_rows_kernel: the row is read once
+// and kept in registers through the two reductions and the encode. Row r uses
+// modulation vectors b = r / rows_per_batch (shift/scale [B, cols], batch
+// stride mod_stride).
+template <int CPL, bool FULL>
+__global__ __launch_bounds__(256) void ln_mod_quantize_kernel(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t rows_per_batch,
+    const uint16_t* __restrict__ shift, const uint16_t* __restrict__ scl, int64_t mod_stride, float eps,
+    float amax_floor, uint8_t* __restrict__ q, float* __restrict__ scale) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const float inv_cols = 1.0f / (float)cols;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows;
+         row += (int64_t)gridDim.x * 4) {  // grid-stride; whole waves, no barrier
+        const uint16_t* xr = x + row * cols;
+        const int nchunks = (int)(cols >> 3);
+        const int64_t b = row / rows_per_batch;
+        const uint16_t* sh = shift + b * mod_stride;
+        const uint16_t* sc = scl + b * mod_stride;
+        // every load of the row issued up front (x from HBM, the modulation
+        // vectors from L2), so they are all in flight together
+        uint4 v[CPL], s8[CPL], h8[CPL];
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (FULL || c < nchunks) v[i] = *reinterpret_cast<const uint4*>(xr + (int64_t)c * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (FULL || c < nchunks) {
+                s8[i] = *reinterpret_cast<const uint4*>(sc + (int64_t)c * 8);
+                h8[i] = *reinterpret_cast<const uint4*>(sh + (int64_t)c * 8);
+            }
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (FULL || c < nchunks) {
+                const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sum = sum + bf16_bits_to_f32(w[j] & 0xffffu);
+                    sum = sum + bf16_bits_to_f32(w[j] >> 16);
+                }
+            }
+        }
+        const float mean = group_sum<64>(sum) * inv_cols;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (FULL || c < nchunks) {
+                const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float d0 = bf16_bits_to_f32(w[j] & 0xffffu) - mean;
+                    const float d1 = bf16_bits_to_f32(w[j] >> 16) - mean;
+                    ss = ss + d0 * d0;
+                    ss = ss + d1 * d1;
+                }
+            }
+        }
+        const float rstd = 1.0f / sqrtf(group_sum<64>(ss) * inv_cols + eps);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c = lane + i * 64;
+            if (FULL || c < nchunks) {
+                uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+                const uint32_t ws[4] = {s8[i].x, s8[i].y, s8[i].z, s8[i].w};
+                const uint32_t wh[4] = {h8[i].x, h8[i].y, h8[i].z, h8[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // each bf16 rounding is one v_cvt_pk_bf16_f32 for the pair
+                    const uint32_t y = f32x2_to_bf16x2((bf16_lo(w[j]) - mean) * rstd,
+                                                       (bf16_hi(w[j]) - mean) * rstd);
+                    const uint32_t a = f32x2_to_bf16x2(1.0f + bf16_lo(ws[j]), 1.0f + bf16_hi(ws[j]));
+                    const uint32_t m = f32x2_to_bf16x2(bf16_lo(y) * bf16_lo(a), bf16_hi(y) * bf16_hi(a));
+                    w[j] = f32x2_to_bf16x2(bf16_lo(m) + bf16_lo(wh[j]), bf16_hi(m) + bf16_hi(wh[j]));
+                    amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
+                }
+                v[i] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+        amax = group_max<64>(amax);
+        const float s = fmaxf(amax, amax_floor) / kE4M3Max;
+        if (lane == 0) scale[row] = s;
+        const Quot d(s);
+        uint8_t* qr = q + row * cols;
+        d.with_form([&](auto form) {
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const int c = lane + i * 64;
+                if (FULL || c < nchunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = encode8<decltype(form)::value>(v[i], d);
+            }
+        });
     }
 }
 
@@ -106,15 +227,15 @@ __global__ __launch_bounds__(256) void quantize_blockwise_kernel(
     const float s = fmaxf(amax, 1e-4f) / kE4M3Max;
     if (threadIdx.x == 0) scale[blockIdx.x * gridDim.y + blockIdx.y] = s;
     const Quot d(s);
+    d.with_form([&](auto form) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int id = threadIdx.x + i * 256;
-        const int64_t r = r0 + (id >> 4);
-        const int64_t c = c0 + (id & 15) * 8;
-        if (r < rows) {
-            *reinterpret_cast<uint2*>(q + r * cols + c) = encode8(v[i], d);
+        for (int i = 0; i < 8; ++i) {
+            const int id = threadIdx.x + i * 256;
+            const int64_t r = r0 + (id >> 4);
+            const int64_t c = c0 + (id & 15) * 8;
+            if (r < rows) *reinterpret_cast<uint2*>(q + r * cols + c) = encode8<decltype(form)::value>(v[i], d);
         }
-    }
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -200,22 +321,9 @@ __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
         amax = group_max<16>(amax);
         const float qmax = FMT == HN_KV_FP8 ? kE4M3Max : 127.0f;
         const float s = amax > 0.0f ? amax / qmax : 1.0f;
-        const Quot d(s);
-        uint32_t lo, hi;
-        if (FMT == HN_KV_FP8) {
-            lo = e4m3_encode4(d(f[0]), d(f[1]), d(f[2]), d(f[3]));
-            hi = e4m3_encode4(d(f[4]), d(f[5]), d(f[6]), d(f[7]));
-        } else {
-            lo = hi = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lo |= int8_code(d(f[j])) << (8 * j);
-                hi |= int8_code(d(f[j + 4])) << (8 * j);
-            }
-        }
         const int64_t tt = rt[k] + a.start;
         *reinterpret_cast<uint2*>(a.q[sel] + rb[k] * a.qs0 + tt * a.qs1 + rh[k] * a.qs2 + lane16 * 8) =
-            make_uint2(lo, hi);
+            codes8<FMT == HN_KV_FP8>(f, Quot(s));
         if (lane16 == 0) a.s[sel][rb[k] * a.ss0 + tt * a.ss1 + rh[k] * a.ss2] = s;
     }
     }
@@ -308,6 +416,45 @@ extern "C" int hn_quantize_rows_fp8(const void* x, int64_t rows, int64_t cols,
 #undef HN_ROWS_CASE
     return fail(HN_E_ARG, "hn_quantize_rows_fp8: unsupported width");
     return check_launch("hn_quantize_rows_fp8");
+}
+
+extern "C" int hn_ln_mod_quantize_fp8(const void* x, int64_t rows, int64_t cols, int64_t rows_per_batch,
+                                      const void* shift, const void* scale_mod, int64_t mod_stride, float eps,
+                                      float amax_floor, void* q, float* scale, void* stream) {
+    HN_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 8192, HN_E_ARG,
+               "hn_ln_mod_quantize_fp8: cols must be a positive multiple of 8 and <= 8192");
+    HN_REQUIRE(rows_per_batch > 0 && mod_stride >= cols && mod_stride % 8 == 0, HN_E_ARG,
+               "hn_ln_mod_quantize_fp8: invalid rows_per_batch or modulation stride");
+    HN_REQUIRE(eps >= 0.0f && amax_floor >= 0.0f, HN_E_ARG, "hn_ln_mod_quantize_fp8: negative eps or floor");
+    HN_REQUIRE(aligned(x, 16) && aligned(shift, 16) && aligned(scale_mod, 16) && aligned(q, 8) &&
+                   aligned(scale, 4),
+               HN_E_ARG, "hn_ln_mod_quantize_fp8: x, shift, scale_mod must be 16-byte and q 8-byte aligned");
+    if (rows == 0) return HN_OK;
+    HN_REQUIRE(x && shift && scale_mod && q && scale, HN_E_ARG, "hn_ln_mod_quantize_fp8: null pointer");
+    HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_ln_mod_quantize_fp8: too many rows");
+    const int per_lane = (int)((cols / 8 + 63) / 64);  // 16-byte chunks per lane, <= 16
+    const dim3 grid((unsigned)stream_grid((rows + 3) / 4, 8));
+    hipStream_t st = (hipStream_t)stream;
+#define HN_LNQ_CASE(N)                                                                                  \
+    if (per_lane <= N) {                                                                                \
+        if (cols == N * 512)                                                                            \
+            ln_mod_quantize_kernel<N, true><<<grid, 256, 0, st>>>(                                      \
+                (const uint16_t*)x, rows, cols, rows_per_batch, (const uint16_t*)shift,                 \
+                (const uint16_t*)scale_mod, mod_stride, eps, amax_floor, (uint8_t*)q, scale);           \
+        else                                                                                            \
+            ln_mod_quantize_kernel<N, false><<<grid, 256, 0, st>>>(                                     \
+                (const uint16_t*)x, rows, cols, rows_per_batch, (const uint16_t*)shift,                 \
+                (const uint16_t*)scale_mod, mod_stride, eps, amax_floor, (uint8_t*)q, scale);           \
+        return check_launch("hn_ln_mod_quantize_fp8");                                                  \
+    }
+    HN_LNQ_CASE(1)
+    HN_LNQ_CASE(2)
+    HN_LNQ_CASE(4)
+    HN_LNQ_CASE(6)
+    HN_LNQ_CASE(8)
+    HN_LNQ_CASE(16)
+#undef HN_LNQ_CASE
+    return fail(HN_E_ARG, "hn_ln_mod_quantize_fp8: unsupported width");
 }
 
 extern "C" int hn_quantize_blockwise_fp8(const void* x, int64_t rows, int64_t cols, void* q,

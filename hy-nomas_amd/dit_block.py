@@ -3,12 +3,14 @@ multi-block AR chunk step built from it (BASELINE configs 4 and 5).
 
 Block math follows the reference's inference pre/post functions
 (hymm/models/dit/modules/nomas_compile_prepost.py:14-99) for the image stream:
-adaLN modulation from silu(vec); LayerNorm (eps 1e-6, no affine) + modulate;
+adaLN modulation from silu(vec); LayerNorm (eps 1e-6, no affine) + modulate,
+fused with the per-token FP8 quantization of the QKV input into one kernel;
 Q/K/V projection (fused into one 3072 -> 9216 FP8 GEMM); per-head RMSNorm
 (fp32, eps 1e-6, weight); interleaved-pair RoPE in fp32 over (t, h, w) with
 axes [16, 56, 56] and theta 256 (posemb_layers.py:191-260,401-453); cached
 attention (FP8 cache history + this chunk's bf16 K/V); out-projection and
-gated residual; LayerNorm + modulate; FFN fc1 with GELU-tanh fused into the
+gated residual; LayerNorm + modulate (fused with fc1's input quantization as
+above); FFN fc1 with GELU-tanh fused into the
 GEMM epilogue, fc2; gated residual. The AR step follows
 hymm/pipeline/causal_ar.py:2348-2432,2624-2645,2852: N denoising passes
 without cache writes, one cache-write pass, then the valid length advances.
@@ -23,7 +25,7 @@ import torch.nn.functional as F
 
 from . import ops
 from .cache_attention import chunk_attention
-from .dit_fp8_linear import FP8StoredLinear, fp8_linear
+from .dit_fp8_linear import FP8StoredLinear, fp8_linear, fp8_linear_codes
 from .fp8_kv_cache import make_fp8_kv_block, quantize_kv_pair_into
 from .metrics import stage
 
@@ -52,7 +54,7 @@ class FP8DiTBlock(nn.Module):
 
     def __init__(self, hidden: int = 3072, heads: int = 24, mlp_ratio: int = 4,
                  qk_eps: float = 1e-6, *, device=None, generator=None,
-                 validate_kv_writes: bool = True):
+                 validate_kv_writes: bool = True, fuse_ln_quant: bool = True):
         super().__init__()
         self.hidden, self.heads, self.head_dim = hidden, heads, hidden // heads
         self.qk_eps = qk_eps
@@ -60,6 +62,9 @@ class FP8DiTBlock(nn.Module):
         # as quantize_kv_pair_into does (one host sync per write pass). False:
         # the write is fused into the QK norm/RoPE kernel, unvalidated.
         self.validate_kv_writes = validate_kv_writes
+        # True: LayerNorm + modulate + the per-token FP8 quantization of the QKV
+        # and fc1 inputs run as one kernel (ops.ln_modulate_quantize_fp8).
+        self.fuse_ln_quant = fuse_ln_quant
         kw = dict(device=device, dtype=torch.bfloat16)
 
         def lin(i, o):
@@ -77,6 +82,9 @@ class FP8DiTBlock(nn.Module):
         self.q_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
         self.k_norm = nn.Parameter(torch.ones(self.head_dim, **kw))
 
+    def _fused(self, linear) -> bool:
+        return self.fuse_ln_quant and isinstance(linear, FP8StoredLinear)
+
     def pre_attention(self, img, vec, cos, sin, kv_cache=None, cache_start: int = 0):
         """Image-stream half of nomas_compile_prepost.pre_attention (:29-72):
         adaLN parts, LayerNorm + modulate, fused FP8 QKV, then per-head RMSNorm
@@ -88,9 +96,15 @@ class FP8DiTBlock(nn.Module):
         H, D = self.heads, self.head_dim
         with stage("modulation"):
             parts = F.linear(F.silu(vec), self.mod.weight, self.mod.bias).chunk(6, dim=-1)
-            x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
+            if self._fused(self.qkv):
+                qx, sx = ops.ln_modulate_quantize_fp8(img, parts[0], parts[1], 1e-6)
+            else:
+                x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
         with stage("qkv_fp8"):
-            qkv = fp8_linear(self.qkv, x).view(B, L, 3, H, D)
+            if self._fused(self.qkv):
+                qkv = fp8_linear_codes(self.qkv, qx, sx).view(B, L, 3, H, D)
+            else:
+                qkv = fp8_linear(self.qkv, x).view(B, L, 3, H, D)
         # select views (not unbind's multi-output views), so the in-place
         # norm/RoPE may modify them
         q, k, v = qkv.select(2, 0), qkv.select(2, 1), qkv.select(2, 2)
@@ -110,8 +124,12 @@ class FP8DiTBlock(nn.Module):
         B, L, C = img.shape
         with stage("post_fp8"):
             img = img + fp8_linear(self.proj, attn.reshape(B, L, C)) * parts[2].unsqueeze(1)
-            h = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[3], parts[4])
-            h = fp8_linear(self.fc1, h, gelu=True)
+            if self._fused(self.fc1):
+                qh, sh = ops.ln_modulate_quantize_fp8(img, parts[3], parts[4], 1e-6)
+                h = fp8_linear_codes(self.fc1, qh, sh, gelu=True).view(B, L, -1)
+            else:
+                h = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[3], parts[4])
+                h = fp8_linear(self.fc1, h, gelu=True)
             h = fp8_linear(self.fc2, h)
             img = img + h * parts[5].unsqueeze(1)
         return img

@@ -85,6 +85,15 @@ class FP8StoredLinear(nn.Module):
         return y.reshape(*x.shape[:-1], self.out_features)
 
 
+def fp8_linear_codes(module: "FP8StoredLinear", qx: torch.Tensor, sx: torch.Tensor,
+                     gelu: bool = False) -> torch.Tensor:
+    """The FP8 linear on activations already quantized per token (codes e4m3
+    [M, in], scales fp32 [M]), e.g. by ops.ln_modulate_quantize_fp8."""
+    bias = None if module.bias is None else module.bias.detach().to(torch.bfloat16)
+    return ops.gemm_fp8_rowcol(qx, module.weight_q, sx, module.weight_scale, bias,
+                               L.HN_ACT_GELU_TANH if gelu else L.HN_ACT_NONE)
+
+
 def linear_weight(module: nn.Module) -> torch.Tensor:
     if isinstance(module, FP8StoredLinear):
         return module.dequant_weight()

@@ -58,6 +58,39 @@ def _(x, scale_mode=L.HN_SCALE_CLAMP, amax_floor=1e-4):
     return x.new_empty(x.shape, dtype=FP8), x.new_empty(x.shape[:-1], dtype=torch.float32)
 
 
+@torch.library.custom_op("hy_nomas_amd::ln_modulate_quantize_fp8", mutates_args=())
+def ln_modulate_quantize_fp8(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                             eps: float = 1e-6,
+                             amax_floor: float = 1e-4) -> tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm (no affine) + adaLN modulate + per-token e4m3 quantization of a
+    bf16 [B, L, C] tensor in one pass: the codes and scales of
+    quantize_rows_fp8(modulate(layer_norm(x), shift, scale)) with shift and
+    scale bf16 [B, C] (nomas_compile_prepost.py:14-15,40-43,81-84). Returns
+    codes [B*L, C] and fp32 scales [B*L]."""
+    _gpu(x, shift, scale)
+    if x.dtype != torch.bfloat16 or shift.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16:
+        raise TypeError("ln_modulate_quantize_fp8 expects bf16 tensors")
+    if x.ndim != 3 or shift.shape != (x.shape[0], x.shape[2]) or scale.shape != shift.shape:
+        raise ValueError("ln_modulate_quantize_fp8: x [B, L, C] with shift and scale [B, C]")
+    x = x.contiguous()
+    shift = shift.contiguous()
+    scale = scale.contiguous()
+    B, Lt, C = x.shape
+    q = torch.empty((B * Lt, C), dtype=FP8, device=x.device)
+    s = torch.empty((B * Lt,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        L.check(L.load().hn_ln_mod_quantize_fp8(
+            x.data_ptr(), B * Lt, C, max(Lt, 1), shift.data_ptr(), scale.data_ptr(), C, eps,
+            amax_floor, q.data_ptr(), s.data_ptr(), _stream(x)), "hn_ln_mod_quantize_fp8")
+    return q, s
+
+
+@ln_modulate_quantize_fp8.register_fake
+def _(x, shift, scale, eps=1e-6, amax_floor=1e-4):
+    n = x.shape[0] * x.shape[1]
+    return x.new_empty((n, x.shape[2]), dtype=FP8), x.new_empty((n,), dtype=torch.float32)
+
+
 @torch.library.custom_op("hy_nomas_amd::quantize_blockwise_fp8", mutates_args=())
 def quantize_blockwise_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """128x128 blockwise e4m3 codes [M,K] and scales [ceil(M/128), K/128]."""

@@ -66,6 +66,19 @@ int hn_quantize_rows_fp8(const void *x, int64_t rows, int64_t cols, int64_t row_
                          int scale_mode, float amax_floor, void *q, float *scale,
                          void *stream);
 
+/* LayerNorm (no affine, eps) + adaLN modulate + per-token FP8 quantization,
+ * fused: o = bf16(bf16(bf16(LN(x)) * bf16(1 + scale_mod[b])) + shift[b]), then
+ * the hn_quantize_rows_fp8 recipe (HN_SCALE_CLAMP, amax_floor) on o.
+ * x: bf16 [rows, cols] contiguous; shift, scale_mod: bf16 [B, cols] with batch
+ * stride mod_stride (elements), row r using batch r / rows_per_batch; q: e4m3
+ * [rows, cols]; scale: fp32 [rows]. cols % 8 == 0, cols <= 8192.
+ * Replaces the LayerNorm + _modulate in front of the block's FP8 linears,
+ * nomas_compile_prepost.py:14-15,40-43 (QKV) and :81-84 (fc1), together with
+ * the linear's activation quantizer (cutlass_fp8.py:35-41,49). */
+int hn_ln_mod_quantize_fp8(const void *x, int64_t rows, int64_t cols, int64_t rows_per_batch,
+                           const void *shift, const void *scale_mod, int64_t mod_stride, float eps,
+                           float amax_floor, void *q, float *scale, void *stream);
+
 /* 128x128 blockwise FP8 quantization, rows zero-padded to a multiple of 128.
  * x: bf16 [rows, cols] contiguous; q: e4m3 [rows, cols]; scale: fp32
  * [ceil(rows/128), cols/128]; cols % 128 == 0. Scale rule HN_SCALE_CLAMP with

@@ -18,6 +18,7 @@ Reference recipes followed (file:line in the upstream repository):
   * KV decode                          hymm/models/dit/modules/int8_kv_cache.py:182-205
   * W8 weight quant (INT8-compat)      hymm/models/dit/modules/int8_stored_bf16_linear.py:46-61
   * dequantize-then-matmul             hymm/models/dit/modules/int8_stored_bf16_linear.py:82-94
+  * LayerNorm + adaLN modulate         hymm/models/dit/modules/nomas_compile_prepost.py:14-15,40-43,81-84
   * blockwise GEMM contract            hymm/models/vae/pixelumm_decoder/csrc/cutlass_fp8.cu:20-57
   * cached attention semantics         hymm/models/dit/nomas_cpt.py:464-685,771-781 and
                                        hymm/models/dit/modules/attention/range_attention.py:212-239
@@ -128,6 +129,65 @@ def quantize_rows_fp8(x_bits: np.ndarray, mode: int = SCALE_CLAMP,
     lib().hn_oracle_quantize_rows_fp8(_ptr(x_bits), rows, cols, cols, mode,
                                       ctypes.c_float(floor), _ptr(q), _ptr(s))
     return q, s
+
+
+def ln_modulate_bf16(x_bits: np.ndarray, shift_bits: np.ndarray, scale_bits: np.ndarray,
+                     eps: float = 1e-6, rows_per_batch: int | None = None) -> np.ndarray:
+    """LayerNorm (no affine) + adaLN modulate of bf16 rows, as bf16 bits:
+    y = bf16(F.layer_norm(x, eps)), o = bf16(bf16(y * bf16(1 + scale)) + shift)
+    (nomas_compile_prepost.py:14-15,40-43,81-84: bf16 tensor ops, each
+    rounding once, round to nearest even). Row r uses shift / scale row
+    r // rows_per_batch ([B, C]).
+
+    The fp32 mean and variance restate the GPU kernel's fixed summation order
+    (hn_ln_mod_quantize_fp8): lane l of 64 adds its values in storage order
+    (8-value chunks l, l + 64, ...), then the lanes combine by xor butterfly;
+    mean = sum * fp32(1 / C), var = sum((x - mean)^2) * fp32(1 / C), rstd =
+    1 / sqrt(var + eps), every step one correctly rounded fp32 operation
+    (numpy float32). Pinned against a float64 LayerNorm and torch's CPU
+    F.layer_norm (at most one bf16 ulp apart, at rounding boundaries) in
+    tests/test_oracle.py."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, cols = x_bits.shape
+    if cols % 8:
+        raise ValueError("cols must be a multiple of 8")
+    rpb = rows if rows_per_batch is None else int(rows_per_batch)
+    x = bf16_bits_to_f32(x_bits)
+    nch = cols // 8
+    lanes = np.arange(64)
+
+    def wave_sum(vals):  # vals float32 [rows, nch, 8] -> float32 [rows]
+        part = np.zeros((rows, 64), dtype=np.float32)
+        for c0 in range(0, nch, 64):
+            cnt = min(64, nch - c0)
+            for k in range(8):
+                part[:, :cnt] = part[:, :cnt] + vals[:, c0:c0 + cnt, k]
+        off = 32
+        while off:
+            part = part + part[:, lanes ^ off]
+            off >>= 1
+        return part[:, 0]
+
+    inv_cols = np.float32(1.0) / np.float32(cols)
+    xc = x.reshape(rows, nch, 8)
+    mean = (wave_sum(xc) * inv_cols).astype(np.float32)
+    d = (xc - mean[:, None, None]).astype(np.float32)
+    var = (wave_sum((d * d).astype(np.float32)) * inv_cols).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    y = bf16_bits_to_f32(f32_to_bf16_bits((d * rstd[:, None, None]).astype(np.float32).reshape(rows, cols)))
+    b = np.arange(rows) // rpb
+    sc = bf16_bits_to_f32(np.asarray(scale_bits, dtype=np.uint16))[b]
+    sh = bf16_bits_to_f32(np.asarray(shift_bits, dtype=np.uint16))[b]
+    a = bf16_bits_to_f32(f32_to_bf16_bits((np.float32(1.0) + sc).astype(np.float32)))
+    m = bf16_bits_to_f32(f32_to_bf16_bits((y * a).astype(np.float32)))
+    return f32_to_bf16_bits((m + sh).astype(np.float32))
+
+
+def ln_modulate_quantize_fp8(x_bits, shift_bits, scale_bits, eps: float = 1e-6,
+                             rows_per_batch: int | None = None):
+    """ln_modulate_bf16 followed by the per-token FP8 quantizer (SCALE_CLAMP,
+    floor 1e-4): the fused hn_ln_mod_quantize_fp8 (codes u8 [R, C], scale f32 [R])."""
+    return quantize_rows_fp8(ln_modulate_bf16(x_bits, shift_bits, scale_bits, eps, rows_per_batch))
 
 
 def quantize_blockwise_fp8(x_bits: np.ndarray):

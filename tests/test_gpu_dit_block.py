@@ -193,6 +193,35 @@ def test_block_end_to_end(dev, update_cache):
         assert torch.equal(cache["v"][:, hist:hist + L].view(torch.uint8), check["v"].view(torch.uint8))
 
 
+def test_block_fused_ln_quant_matches_unfused(dev):
+    """The fused LayerNorm + modulate + FP8 quant kernel against the block's
+    unfused torch path (F.layer_norm, bf16 modulate, quantize_rows_fp8): they
+    differ only where a LayerNorm output sits on a bf16 rounding boundary."""
+    blk, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev)
+    ops = pkg_module("ops")
+    calls = []
+    real = ops.ln_modulate_quantize_fp8
+
+    def counted(*a, **k):
+        calls.append(a[0].shape)
+        return real(*a, **k)
+
+    ops.ln_modulate_quantize_fp8 = counted
+    try:
+        with torch.no_grad():
+            fused = blk(img, vec, cos, sin, cache, hist, update_cache=False)
+            assert len(calls) == 2, calls                # pre-attention LN and the FFN's LN
+            blk.fuse_ln_quant = False
+            unfused = blk(img, vec, cos, sin, cache, hist, update_cache=False)
+            assert len(calls) == 2, calls
+    finally:
+        ops.ln_modulate_quantize_fp8 = real
+    x = _cpu(img).float()
+    rel = _rel(_cpu(fused).float() - x, _cpu(unfused).float() - x)
+    print(f"fused vs unfused block update rel-L2 {rel:.3e}", flush=True)
+    assert rel <= 2e-3
+
+
 def test_ar_chunk_loop_structure(dev):
     """Two chunks through a 2-block model: each chunk runs the denoising passes
     without cache writes, then one write pass; the valid length advances by a

@@ -186,3 +186,53 @@ def test_kv_write_twice_is_deterministic(dev):
     kvc.quantize_kv_pair_into(b, x, x, 0)
     assert torch.equal(a["k"].view(torch.uint8), b["k"].view(torch.uint8))
     assert torch.equal(a["v_scale"], b["v_scale"])
+
+
+# LayerNorm + adaLN modulate + per-token FP8 quant, fused (the block's path into
+# its QKV and fc1 linears).
+
+def _ln_inputs(dev, B, L, C, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = (torch.randn(B, L, C, device=dev, generator=g) * 3 + 0.5).to(torch.bfloat16)
+    sh = (torch.randn(B, C, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    sc = (torch.randn(B, C, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    return x, sh, sc
+
+
+@pytest.mark.parametrize("B,L,C", [(1, 300, 3072), (2, 130, 640), (1, 5, 8), (1, 10800, 3072)])
+def test_ln_modulate_quantize_bit_exact(O, dev, B, L, C):
+    """Codes and scales equal the oracle's (its LayerNorm restates the kernel's fp32
+    summation order; the modulate and the quantizer are the reference recipes)."""
+    print(f"case ln-mod-quant {B}x{L}x{C}", flush=True)
+    ops = pkg_module("ops")
+    x, sh, sc = _ln_inputs(dev, B, L, C, B * L + C)
+    q, s = ops.ln_modulate_quantize_fp8(x, sh, sc, 1e-6)
+    qo, so = O.ln_modulate_quantize_fp8(bf16_bits(x.reshape(B * L, C)), bf16_bits(sh), bf16_bits(sc), 1e-6,
+                                        rows_per_batch=L)
+    assert np.array_equal(u8(q), qo)
+    assert np.array_equal(s.cpu().numpy(), so)
+
+
+def test_ln_modulate_quantize_matches_unfused_torch_path(dev):
+    """Against F.layer_norm + the bf16 modulate ops + quantize_rows_fp8 on the GPU
+    (torch's own LayerNorm summation): codes agree except where a LayerNorm output
+    sits on a bf16 rounding boundary."""
+    ops = pkg_module("ops")
+    B, L, C = 1, 2048, 3072
+    x, sh, sc = _ln_inputs(dev, B, L, C, 5)
+    q, s = ops.ln_modulate_quantize_fp8(x, sh, sc, 1e-6)
+    y = torch.nn.functional.layer_norm(x, (C,), eps=1e-6)
+    mod = y * (1 + sc.unsqueeze(1)) + sh.unsqueeze(1)
+    qr, sr = ops.quantize_rows_fp8(mod.reshape(B * L, C))
+    agree = (u8(q) == u8(qr)).mean()
+    assert agree >= 0.999, agree
+    assert torch.allclose(s, sr, rtol=2 ** -7, atol=0)
+
+
+def test_ln_modulate_quantize_rejects_bad_shapes(dev):
+    ops = pkg_module("ops")
+    x, sh, sc = _ln_inputs(dev, 1, 4, 64, 1)
+    with pytest.raises(ValueError):
+        ops.ln_modulate_quantize_fp8(x, sh[:, :32], sc, 1e-6)
+    with pytest.raises(TypeError):
+        ops.ln_modulate_quantize_fp8(x.float(), sh, sc, 1e-6)

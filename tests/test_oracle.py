@@ -129,6 +129,69 @@ def test_row_quant_matches_torch_reference_recipe(O):
     assert np.array_equal(q, q_kv) and np.array_equal(s, s_kv.numpy()[:, 0])
 
 
+# ------------------------------------------------ LayerNorm + adaLN modulate
+
+def _ln_rows(rng, rows, cols):
+    x = torch.from_numpy((rng.standard_normal((rows, cols)) * 3 + 0.5).astype(np.float32)).to(torch.bfloat16)
+    return x
+
+
+def _ulp_gap(a_bits, b_bits):
+    """Distance in bf16 steps between finite same-sign or small values."""
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    ia = np.where(a & 0x8000, -(a & 0x7FFF), a)
+    ib = np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("rows,cols", [(48, 3072), (16, 640), (8, 8)])
+def test_ln_modulate_layernorm_matches_float64_and_torch(O, rows, cols):
+    """With scale = shift = 0 the output is bf16(LayerNorm(x)). Against a float64
+    LayerNorm and torch's CPU F.layer_norm (bf16 in, bf16 out): equal except at
+    bf16 rounding boundaries, where the fp32 sums may land one ulp apart, and
+    near zero, where the fp32 mean's rounding (~1e-7 on a unit-variance output)
+    spans several ulps of a tiny value."""
+    rng = np.random.default_rng(rows + cols)
+    x = _ln_rows(rng, rows, cols)
+    zeros = np.zeros((1, cols), dtype=np.uint16)
+    y = O.ln_modulate_bf16(bf16_bits(x), zeros, zeros, 1e-6)
+    xd = x.double()
+    ref64 = ((xd - xd.mean(-1, keepdim=True)) / torch.sqrt(xd.var(-1, unbiased=False, keepdim=True) + 1e-6))
+    r64 = bf16_bits(ref64.float().to(torch.bfloat16))
+    rt = bf16_bits(torch.nn.functional.layer_norm(x, (cols,), eps=1e-6))
+    for ref in (r64, rt):
+        gap = _ulp_gap(y, ref)
+        absdiff = np.abs(O.bf16_bits_to_f32(y) - O.bf16_bits_to_f32(ref))
+        assert ((gap <= 1) | (absdiff <= 1e-6)).all() and (gap == 0).mean() >= 0.999
+
+
+def test_ln_modulate_modulate_matches_torch_bf16_ops(O):
+    """The modulate step is exactly torch's bf16 tensor ops x * (1 + scale) + shift
+    (nomas_compile_prepost.py:14-15) applied to the bf16 LayerNorm output."""
+    rng = np.random.default_rng(11)
+    rows, cols = 32, 3072
+    x = _ln_rows(rng, rows, cols)
+    zeros = np.zeros((1, cols), dtype=np.uint16)
+    y = torch.from_numpy(O.ln_modulate_bf16(bf16_bits(x), zeros, zeros, 1e-6).view(np.int16)).view(torch.bfloat16)
+    sc = (torch.randn(2, cols) * 0.5).to(torch.bfloat16)
+    sh = (torch.randn(2, cols) * 0.5).to(torch.bfloat16)
+    o = O.ln_modulate_bf16(bf16_bits(x), bf16_bits(sh), bf16_bits(sc), 1e-6, rows_per_batch=rows // 2)
+    yb = y.view(2, rows // 2, cols)
+    ref = yb * (1 + sc.unsqueeze(1)) + sh.unsqueeze(1)
+    assert np.array_equal(o, bf16_bits(ref.reshape(rows, cols)))
+
+
+def test_ln_modulate_constant_row_gives_shift(O):
+    """A constant row has zero variance: LN gives 0, so the output is the shift exactly."""
+    cols = 256
+    x = np.full((3, cols), 0x3FC0, dtype=np.uint16)  # 1.5
+    sh = bf16_bits(torch.randn(1, cols).to(torch.bfloat16))
+    sc = bf16_bits(torch.randn(1, cols).to(torch.bfloat16))
+    o = O.ln_modulate_bf16(x, sh, sc, 1e-6)
+    assert np.array_equal(o, np.repeat(sh, 3, axis=0))
+
+
 def test_blockwise_quant_known_answers_and_padding(O):
     m, k = 130, 256
     x = np.zeros((m, k), np.float32)
