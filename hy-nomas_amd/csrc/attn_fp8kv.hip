@@ -51,7 +51,14 @@ constexpr int VT_BYTES = D * VTROW;
 constexpr int STAGE = K_BYTES + VT_BYTES;
 // Per-key scales of a tile in flight ([0, 64) K, [64, 128) V), two buffers.
 constexpr int SB_FLOATS = 2 * BKV;
-constexpr int SMEM = 2 * STAGE + 2 * SB_FLOATS * 4;
+// K/V stages in LDS: three for the 8-wave shape (one workgroup per CU), so
+// that a tile is written two tiles ahead of its use and one barrier per tile
+// suffices; two for the 4-wave shape, whose two workgroups per CU could not
+// hold three each.
+template <int NW>
+constexpr int stages() { return NW == 8 ? 3 : 2; }
+template <int NW>
+constexpr int smem_bytes() { return stages<NW>() * STAGE + 2 * SB_FLOATS * 4; }
 
 // Workgroup shape for NW (4 or 8) waves.
 template <int NW>
@@ -502,8 +509,9 @@ HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 
 template <int FMT, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     constexpr int BQ = Shape<NW>::BQ;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
-    float* const sbuf = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][128]
+    constexpr int NS = stages<NW>();
+    __shared__ __attribute__((aligned(16))) uint8_t smem[smem_bytes<NW>()];
+    float* const sbuf = reinterpret_cast<float*>(smem + NS * STAGE);  // [2][128]
 
     // XCD-aware work order: workgroup ids are dealt round-robin to the 8 XCDs,
     // so id % 8 picks a contiguous range of work items -- the query tiles of
@@ -607,87 +615,179 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     CacheRegs<NW> regs;
     regs.s = 0.0f;
 
-    // Software pipeline over half tiles. Per tile u = t - t_begin (stage
-    // u % 2; the next tile in the other stage; scales of tile u in buffer u % 2):
+    // Software pipeline over half tiles. Tile t (u = t - t_begin) is in
+    // stage u % NS; during it the wave writes tile t + NS - 1 (dequantized from
+    // the prefetch registers, scales from buffer (u + NS - 1) % 2) to stage
+    // (u + NS - 1) % NS and fetches the codes and scales of tile t + NS:
     //   half 0: rebase; S(t, kb 1) || probs(kb 0)
-    //           PV(t, kb 0) || max(kb 1), K of t + 1 written; K codes + scales of t + 2 fetched
+    //           PV(t, kb 0) || max(kb 1), K of t + NS - 1 written; K codes +
+    //           scales of t + NS fetched
     //   half 1: rebase; S(t + 1, kb 0) || probs(kb 1)
-    //           PV(t, kb 1) || max(t + 1, kb 0), V^T of t + 1 written; scales of
-    //           t + 2 to buffer u % 2, V codes of t + 2 fetched
-    // Stage reuse: stage (u + 1) % 2 (tile t - 1) is last read by PV in half 1
-    // of t - 1, before the barrier that precedes its K write in half 0 of t;
-    // K of t + 1 is first read after the barrier that ends half 0, V^T of
-    // t + 1 after the barrier that ends half 1. Scale buffer u % 2 (tile t)
-    // was last read in half 1 of t - 1.
-    if (t_end > t_begin) {
-        f32x16 sa, sb;
-        float mxa, mxb;
-        Geom g = geom(t_begin);
-        {
-            if (g.cache) {
-                const TileBase tb = tile_base(p, b, h, g.first);
-                load_k<NW>(p, regs, tb, g.count);
-                load_v<NW>(p, regs, tb, g.count);
+    //           PV(t, kb 1) || max(t + 1, kb 0), V^T of t + NS - 1 written;
+    //           scales of t + NS to buffer (u + NS) % 2, V codes fetched
+    // NS = 2 (the loop below, written for it): K of t + 1 is written in half
+    // 0 and read by S(t + 1) in half 1, so a barrier ends half 0 as well as
+    // the tile. NS = 3 (the generic loop after it): every tile a half
+    // reads was written before the barrier that ended an earlier tile, and
+    // the stage written during tile t (that of t - 1) was last read in half 1
+    // of t - 1, before the barrier ending it; one barrier per tile.
+    // Scale buffer (u + NS) % 2 last served the write of tile t + NS - 2,
+    // during tile t - 2 (NS = 3) or t - 1 (NS = 2), before a barrier.
+    if constexpr (NS == 2) {
+        if (t_end > t_begin) {
+            f32x16 sa, sb;
+            float mxa, mxb;
+            Geom g = geom(t_begin);
+            {
+                if (g.cache) {
+                    const TileBase tb = tile_base(p, b, h, g.first);
+                    load_k<NW>(p, regs, tb, g.count);
+                    load_v<NW>(p, regs, tb, g.count);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
+                    __syncthreads();
+                    store_tile<FMT, NW>(regs, smem, sbuf);
+                } else {
+                    copy_tail_k<NW>(p, b, h, g.first, g.count, smem);
+                    copy_tail_v<NW>(p, b, h, g.first, g.count, smem);
+                }
+                if (t_begin + 1 < t_end) {
+                    const Geom g1 = geom(t_begin + 1);
+                    if (g1.cache) {
+                        const TileBase tb = tile_base(p, b, h, g1.first);
+                        load_k<NW>(p, regs, tb, g1.count);
+                        load_v<NW>(p, regs, tb, g1.count);
+                    }
+                }
+                // Everything issued so far (the Q fragments included) has landed;
+                // inside the loop the only loads in flight are the prefetch.
                 __builtin_amdgcn_s_waitcnt(0);
-                if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
+                if (threadIdx.x < 2 * BKV) sbuf[SB_FLOATS + threadIdx.x] = regs.s;
                 __syncthreads();
-                store_tile<FMT, NW>(regs, smem, sbuf);
-            } else {
-                copy_tail_k<NW>(p, b, h, g.first, g.count, smem);
-                copy_tail_v<NW>(p, b, h, g.first, g.count, smem);
+                sa = s_block(smem + ka_off, qf);
+                mxa = g.full ? raw_max(sa) : mask_raw(sa, 0, half, g.lim);
             }
-            if (t_begin + 1 < t_end) {
-                const Geom g1 = geom(t_begin + 1);
-                if (g1.cache) {
-                    const TileBase tb = tile_base(p, b, h, g1.first);
-                    load_k<NW>(p, regs, tb, g1.count);
-                    load_v<NW>(p, regs, tb, g1.count);
+            for (int t = t_begin; t < t_end; ++t) {
+                const int u = t - t_begin;
+                const uint8_t* st = smem + (u & 1) * STAGE;
+                uint8_t* nst = smem + ((u & 1) ^ 1) * STAGE;
+                const float* nsb = sbuf + ((u & 1) ^ 1) * SB_FLOATS;  // scales of tile t + 1
+                const bool has_next = t + 1 < t_end;
+                const Geom gn = geom(has_next ? t + 1 : t);
+                const bool fetch2 = t + 2 < t_end;
+                const Geom g2 = geom(fetch2 ? t + 2 : t);
+                bf16x8 pf[2];
+
+                // ---- half 0
+                rebase(mxa, c, m, l, o);
+                sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
+                // K of tile t + 1 from the prefetch registers (a tail tile or the
+                // end of the range is handled right after: the K rows of the stage
+                // are not read before the barrier).
+                mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
+                if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
+                if (has_next && !gn.cache) copy_tail_k<NW>(p, b, h, gn.first, gn.count, nst);
+                if (fetch2 && g2.cache) load_k<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                __syncthreads();
+
+                // ---- half 1 (on the last tile the S block of "tile t + 1" reads
+                // stale LDS; its result is never used)
+                rebase(mxb, c, m, l, o);
+                sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
+                mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
+                if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
+                if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
+                if (fetch2 && g2.cache) {
+                    if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                    load_v<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                }
+                __syncthreads();
+                g = gn;
+            }
+        }
+    } else {
+        if (t_end > t_begin) {
+            f32x16 sa, sb;
+            float mxa, mxb;
+            // Prologue: tiles t_begin .. t_begin + NS - 2 written, the codes of
+            // t_begin + NS - 1 in the prefetch registers with their scales in
+            // buffer (NS - 1) % 2. Tiles k < NS - 1: load, scales to buffer k % 2,
+            // barrier, dequantizing write to stage k (buffer k % 2 is rewritten
+            // only after the next barrier, which follows this write).
+#pragma unroll
+            for (int k = 0; k < NS - 1; ++k) {
+                const int t = t_begin + k;
+                if (t >= t_end) break;
+                const Geom gk = geom(t);
+                if (gk.cache) {
+                    const TileBase tb = tile_base(p, b, h, gk.first);
+                    load_k<NW>(p, regs, tb, gk.count);
+                    load_v<NW>(p, regs, tb, gk.count);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    if (threadIdx.x < 2 * BKV) sbuf[(k & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                    __syncthreads();
+                    store_tile<FMT, NW>(regs, smem + k * STAGE, sbuf + (k & 1) * SB_FLOATS);
+                } else {
+                    copy_tail_k<NW>(p, b, h, gk.first, gk.count, smem + k * STAGE);
+                    copy_tail_v<NW>(p, b, h, gk.first, gk.count, smem + k * STAGE);
+                }
+            }
+            if (t_begin + NS - 1 < t_end) {
+                const Geom gk = geom(t_begin + NS - 1);
+                if (gk.cache) {
+                    const TileBase tb = tile_base(p, b, h, gk.first);
+                    load_k<NW>(p, regs, tb, gk.count);
+                    load_v<NW>(p, regs, tb, gk.count);
                 }
             }
             // Everything issued so far (the Q fragments included) has landed;
             // inside the loop the only loads in flight are the prefetch.
             __builtin_amdgcn_s_waitcnt(0);
-            if (threadIdx.x < 2 * BKV) sbuf[SB_FLOATS + threadIdx.x] = regs.s;
+            if (threadIdx.x < 2 * BKV) sbuf[((NS - 1) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
             __syncthreads();
+            Geom g = geom(t_begin);
             sa = s_block(smem + ka_off, qf);
             mxa = g.full ? raw_max(sa) : mask_raw(sa, 0, half, g.lim);
-        }
-        for (int t = t_begin; t < t_end; ++t) {
-            const int u = t - t_begin;
-            const uint8_t* st = smem + (u & 1) * STAGE;
-            uint8_t* nst = smem + ((u & 1) ^ 1) * STAGE;
-            const float* nsb = sbuf + ((u & 1) ^ 1) * SB_FLOATS;  // scales of tile t + 1
-            const bool has_next = t + 1 < t_end;
-            const Geom gn = geom(has_next ? t + 1 : t);
-            const bool fetch2 = t + 2 < t_end;
-            const Geom g2 = geom(fetch2 ? t + 2 : t);
-            bf16x8 pf[2];
+            for (int t = t_begin; t < t_end; ++t) {
+                const int u = t - t_begin;
+                const uint8_t* st = smem + (u % NS) * STAGE;              // tile t
+                const uint8_t* st1 = smem + ((u + 1) % NS) * STAGE;       // tile t + 1
+                uint8_t* wst = smem + ((u + NS - 1) % NS) * STAGE;        // tile t + NS - 1
+                const float* wsb = sbuf + ((u + NS - 1) & 1) * SB_FLOATS; // its scales
+                const bool has_next = t + 1 < t_end;
+                const Geom gn = geom(has_next ? t + 1 : t);
+                const bool write = t + NS - 1 < t_end;
+                const Geom gw = geom(write ? t + NS - 1 : t);
+                const bool fetch = t + NS < t_end;
+                const Geom gf = geom(fetch ? t + NS : t);
+                bf16x8 pf[2];
 
-            // ---- half 0
-            rebase(mxa, c, m, l, o);
-            sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
-            // K of tile t + 1 from the prefetch registers (a tail tile or the
-            // end of the range is handled right after: the K rows of the stage
-            // are not read before the barrier).
-            mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
-            if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
-            if (has_next && !gn.cache) copy_tail_k<NW>(p, b, h, gn.first, gn.count, nst);
-            if (fetch2 && g2.cache) load_k<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
-            __syncthreads();
+                // ---- half 0
+                rebase(mxa, c, m, l, o);
+                sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
+                // K of tile t + NS - 1 from the prefetch registers (a tail tile or
+                // the end of the range is handled right after: the K rows of the
+                // stage are not read before the barrier).
+                mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
+                if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
+                if (write && !gw.cache) copy_tail_k<NW>(p, b, h, gw.first, gw.count, wst);
+                if (fetch && gf.cache) load_k<NW>(p, regs, tile_base(p, b, h, gf.first), gf.count);
+                if (NS == 2) __syncthreads();
 
-            // ---- half 1 (on the last tile the S block of "tile t + 1" reads
-            // stale LDS; its result is never used)
-            rebase(mxb, c, m, l, o);
-            sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
-            mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
-            if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
-            if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
-            if (fetch2 && g2.cache) {
-                if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                load_v<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                // ---- half 1 (on the last tile the S block of "tile t + 1" reads
+                // stale LDS; its result is never used)
+                rebase(mxb, c, m, l, o);
+                sa = step_a(sb, c, m, l, pf, st1 + ka_off, qf);
+                mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
+                if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
+                if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
+                if (fetch && gf.cache) {
+                    if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                    load_v<NW>(p, regs, tile_base(p, b, h, gf.first), gf.count);
+                }
+                __syncthreads();
+                g = gn;
             }
-            __syncthreads();
-            g = gn;
         }
     }
     l += __shfl_xor(l, 32, 64);
