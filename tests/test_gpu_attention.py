@@ -191,6 +191,37 @@ def test_eight_wave_tiles_with_split_remainder(O, dev):
            "8-wave + split remainder")
 
 
+@pytest.mark.parametrize("kv_len,cur_len", [(64, 0), (100, 0), (130, 0), (0, 40), (64, 100), (130, 70)])
+def test_eight_wave_short_key_ranges(O, dev, kv_len, cur_len):
+    """The 8-wave shape (H 128 x 2 whole tiles, every row on it) over 1-4 key
+    tiles: ranges shorter than its three K/V stages, partial last tiles, and
+    FP8 cache tiles followed by bf16 tail tiles; every key visible."""
+    print(f"case attn 8-wave short kv={kv_len} cur={cur_len}", flush=True)
+    ca = pkg_module("cache_attention")
+    kvc = pkg_module("fp8_kv_cache")
+    H, D, Lq = 128, 128, 512
+    if kv_len:
+        cache = _cache_from_chunks(dev, 1, kv_len, H, D, 40 + kv_len)
+    else:
+        cache = kvc.make_fp8_kv_block(1, 64, H, D, device=dev)
+        for buf in cache.values():
+            buf.view(torch.uint8).zero_()
+    q = _q(dev, Lq, H, D, 41)
+    kh, vh = _dequant(O, cache, kv_len)
+    if cur_len:
+        g = torch.Generator(device=dev).manual_seed(42)
+        kc = (torch.randn(1, cur_len, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+        vc = (torch.randn(1, cur_len, H, D, device=dev, generator=g) * 2).to(torch.bfloat16)
+        out = ca.chunk_attention(q, cache, kv_len, k_cur=kc, v_cur=vc)
+        kh = np.concatenate([kh, O.bf16_bits_to_f32(bf16_bits(kc[0]))], 0)
+        vh = np.concatenate([vh, O.bf16_bits_to_f32(bf16_bits(vc[0]))], 0)
+    else:
+        out = ca.chunk_attention(q, cache, kv_len)
+    rows = np.arange(0, Lq, 3)
+    _check(O, out[0, rows].float().cpu().numpy(), O.bf16_bits_to_f32(bf16_bits(q[0, rows])), kh, vh,
+           "8-wave short range")
+
+
 @pytest.mark.parametrize("Lq,kv_len,H", [(128, 86400, 24), (100, 20000, 4), (1, 5000, 2)])
 def test_split_kv_decode_style(O, dev, Lq, kv_len, H):
     """Few queries over a long cache: the key range is split across workgroups
