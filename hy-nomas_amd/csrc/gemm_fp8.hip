@@ -671,24 +671,27 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
 }
 
 // ===========================================================================
-// Overlapped-epilogue row/column kernel (K >= 11 x 128): persistent, one
-// workgroup per CU walking its XCD's tile queue (tile_of order).
+// Overlapped-epilogue row/column kernel (K >= O_MIN_KT x 128): persistent,
+// one workgroup per CU walking its XCD's tile queue (tile_of order).
 //
 // With one wave per SIMD holding a 128 x 128 accumulator, an epilogue's VALU
 // work cannot overlap another wave's MFMAs -- only the same wave's. So the
-// wave carries each finished tile's output into the next tile's K loop:
-//   * after a tile's K loop it converts the accumulator to y = bf16(acc * sa *
-//     sb + bias) (128 VGPRs of packed pairs; the reference's linear output,
-//     rounded to bf16 before the activation as in the reference);
-//   * during the next tile's first nine K steps it applies the activation to
-//     y and writes it out through a 4 KB LDS staging area -- eight passes of
-//     32 rows x 64 columns, one per step, one element per MFMA slot, with the
-//     128-byte row read-back and the stores of pass p in step p + 1.
-// Registers: fragments are read "rolling" into the registers their last MFMA
-// of the slice has just read (slot s = 4 i + j runs MFMA (i, j); B block i is
-// replaced after slot 4 i + 3, A block j after slot 12 + j), 64 VGPRs instead
-// of 128. LDS: four 32 KB stage buffers (two K steps: step s in pair (s + par)
-// & 1), the staging areas and the epilogue parameters (DMA'd in step 0).
+// wave carries half of each finished tile's output into the next tile's K loop:
+//   * after a tile's K loop it converts row blocks 0 .. O_JO - 1 of its
+//     accumulator to y = bf16(acc * sa * sb + bias) (64 VGPRs of packed
+//     pairs; the reference's linear output, rounded to bf16 before the
+//     activation as in the reference) and writes row blocks O_JO .. 3
+//     directly (direct_passes);
+//   * during the next tile's first O_PASSES K steps it applies the activation
+//     to y and writes it out through a 4 KB LDS staging area -- O_PASSES
+//     passes of 32 rows x 64 columns, one per step, one element per MFMA
+//     slot -- with the 128-byte row read-back and the stores of pass p in
+//     step p + 1.
+// Fragments are read "rolling" into the registers their last MFMA of the
+// slice has just read (slot s = 4 i + j runs MFMA (i, j); B block i is
+// replaced after slot 4 i + 3, A block j after slot 12 + j). LDS: four 32 KB
+// stage buffers (two K steps: step s in pair (s + par) & 1), the staging
+// areas and the epilogue parameters (DMA'd in step 0).
 //
 // Step k: half 0 -- MFMAs of slice (k, 0), reads of slice (k, 1); wait for
 // step k + 1 (vmcnt(0)) and barrier; half 1 -- MFMAs of slice (k, 1), reads of
