@@ -681,7 +681,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
 //     accumulator to y = bf16(acc * sa * sb + bias) (64 VGPRs of packed
 //     pairs; the reference's linear output, rounded to bf16 before the
 //     activation as in the reference) and writes row blocks O_JO .. 3
-//     directly (direct_passes);
+//     straight to memory (direct_passes);
 //   * during the next tile's first O_PASSES K steps it applies the activation
 //     to y and writes it out through a 4 KB LDS staging area -- O_PASSES
 //     passes of 32 rows x 64 columns, one per step, one element per MFMA
@@ -845,9 +845,13 @@ HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, i
 }
 
 // Passes 2 j, 2 j + 1 for the row blocks j >= O_JO straight from the
-// accumulator (not carried): scale, bias, activation, staging, stores.
+// accumulator (not carried): scale, bias, activation and stores. A lane holds
+// 4 consecutive columns of one row per (block, vq) and stores them as 8
+// bytes, without the LDS staging of the carried passes: the 8 stores of a
+// pass write every byte of its 32 rows' 128-byte lines, which the L2 merges.
+// (Measured with bias + GELU: 387 against 393 us through the staging area.)
 template <int ACT>
-HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, uint8_t* stg, int64_t m0,
+HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, int64_t m0,
                              int64_t n0, int wm, int wn, int lane) {
     const int h = lane >> 5, r = lane & 31;
 #pragma unroll
@@ -881,11 +885,10 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
                     v[3] = gelu_tanh(__uint_as_float(o.y & 0xffff0000u));
                     o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
                 }
-                const int c = 4 * ii + vq;
-                *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * h) = o;
+                const int64_t m = m0 + wm * 128 + 32 * j + r;
+                const int64_t n = n0 + wn * 128 + nl;
+                if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
             }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) oe_store(p, m0, n0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
     }
 }
 
@@ -1149,7 +1152,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
         }
-        direct_passes<ACT>(p, acc, prm, stg, cm0, cn0, wm, wn, fresh_lane());
+        direct_passes<ACT>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
         convert_tile(acc, y, prm, fresh_lane());
         pm0 = cm0;
         pn0 = cn0;
