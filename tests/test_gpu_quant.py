@@ -95,12 +95,15 @@ def test_kv_quantize_quotient_edge_rows(O, dev, fmt):
     assert np.array_equal(cache["k_scale"].cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
-def test_rows_fp8_strided_input(O, dev):
+@pytest.mark.parametrize("width,lo,hi", [(512, 128, 384), (12288, 1024, 7176)])
+def test_rows_fp8_strided_input(O, dev, width, lo, hi):
+    """A column window of wider rows (16-byte aligned start): one wave per row
+    for 256 columns, one workgroup per row for 6152 (> 4096)."""
     ops = pkg_module("ops")
-    x = _gen((64, 512), 11)
-    view = x.to(dev)[:, 128:384]            # row stride 512, 16-byte aligned start
+    x = _gen((64, width), 11)
+    view = x.to(dev)[:, lo:hi]               # row stride `width`
     q, s = ops.quantize_rows_fp8(view, 0, 1e-4)
-    qo, so = O.quantize_rows_fp8(bf16_bits(x[:, 128:384]))
+    qo, so = O.quantize_rows_fp8(bf16_bits(x[:, lo:hi]))
     assert np.array_equal(u8(q), qo) and np.array_equal(s.cpu().numpy(), so)
 
 
