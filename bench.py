@@ -32,7 +32,8 @@ FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense BF16 MFMA
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 
-# Algorithmic work (see DESIGN.md "Measurement").
+# Workload shapes: the north-star linear, config 1, the config-2 KV write and
+# the config-3 attention (Q of the last chunk over 8 cached chunks).
 NS_M, NS_K, NS_N = 10800, 3072, 12288
 C1_M, C1_K, C1_N = 4096, 3072, 3072
 KV_H, KV_L, KV_D = 24, 10800, 128
@@ -89,7 +90,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the hot path's multi-GPU sharding is design-only (DESIGN.md).", file=sys.stderr)
+              "sharding the hot path over several GPUs (heads for KV write and attention, tokens "
+              "for the linear) is not built.", file=sys.stderr)
         sys.exit(2)
 
     import torch
