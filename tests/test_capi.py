@@ -65,7 +65,22 @@ def test_argument_errors_are_reported_without_a_launch(lib):
     assert lib.hn_qk_norm_rope_kv(3, None, None, None, st, 1, 4, 2, 128, None, None, None, None, 128,
                                   1e-6, None, None, None, None, None, None, 0, None) == -1
     assert "format" in _err(lib)
+    assert lib.hn_quantize_rows_fp8(None, 4, 16392, 16392, 0, 1e-4, None, None, None) == -1
+    assert "16384" in _err(lib)
+    # fused LayerNorm + modulate + quant: width, modulation layout, eps
+    lnq = lib.hn_ln_mod_quantize_fp8
+    assert lnq(None, 4, 100, 4, None, None, 100, 1e-6, 1e-4, None, None, None) == -1
+    assert "multiple of 8" in _err(lib)
+    assert lnq(None, 4, 8200, 4, None, None, 8200, 1e-6, 1e-4, None, None, None) == -1
+    assert "8192" in _err(lib)
+    assert lnq(None, 4, 128, 0, None, None, 128, 1e-6, 1e-4, None, None, None) == -1
+    assert "rows_per_batch" in _err(lib)
+    assert lnq(None, 4, 128, 4, None, None, 64, 1e-6, 1e-4, None, None, None) == -1
+    assert "stride" in _err(lib)
+    assert lnq(None, 4, 128, 4, None, None, 128, -1.0, 1e-4, None, None, None) == -1
+    assert "eps" in _err(lib)
     # zero-size work is a no-op that needs no pointers
+    assert lnq(None, 0, 128, 1, None, None, 128, 1e-6, 1e-4, None, None, None) == L.HN_OK
     assert lib.hn_quantize_rows_fp8(None, 0, 8, 8, 0, 1e-4, None, None, None) == L.HN_OK
     assert lib.hn_gemm_fp8_rowcol(None, None, None, None, None, None, 0, 128, 128, 128, 0, None) == L.HN_OK
 
