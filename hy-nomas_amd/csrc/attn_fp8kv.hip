@@ -829,26 +829,43 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
 
 // Merge of the per-split partial results: with M = max_s m_s,
 // O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (0 when no key was visible).
-// One 128-thread block per (batch, head, query); thread d owns one dimension.
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ ws_o,
+// 8 (batch, head, query) rows per 256-thread block, 32 threads per row, each
+// owning 4 consecutive dimensions: 16-byte loads of the partials and one
+// 8-byte store. Every element is the same chain of operations in split order
+// as with one thread per dimension, so the result does not depend on the
+// block shape.
+constexpr int COMBINE_ROWS = 8;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws_o,
                                                            const float* __restrict__ ws_ml,
                                                            int splits, int64_t rows_per_split,
                                                            int64_t Lq, int64_t H, uint16_t* out,
                                                            int64_t os0, int64_t os1, int64_t os2) {
-    const int64_t r = blockIdx.x;  // (b * H + h) * Lq + q
-    const int d = threadIdx.x;
+    const int64_t r = (int64_t)blockIdx.x * COMBINE_ROWS + (threadIdx.x >> 5);  // (b * H + h) * Lq + q
+    if (r >= rows_per_split) return;
+    const int d = (threadIdx.x & 31) * 4;
     float M = -INFINITY;
     for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, ws_ml[(sp * rows_per_split + r) * 2]);
     const float Muse = M == -INFINITY ? 0.0f : M;
-    float num = 0.0f, den = 0.0f;
+    float den = 0.0f;
+    float num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
     for (int sp = 0; sp < splits; ++sp) {
         const int64_t idx = sp * rows_per_split + r;
-        const float wgt = __builtin_amdgcn_exp2f(ws_ml[idx * 2] - Muse);
-        den = fmaf(wgt, ws_ml[idx * 2 + 1], den);
-        num = fmaf(wgt, ws_o[idx * D + d], num);
+        const float2 ml = *reinterpret_cast<const float2*>(ws_ml + idx * 2);
+        const float4 ov = *reinterpret_cast<const float4*>(ws_o + idx * D + d);
+        const float wgt = __builtin_amdgcn_exp2f(ml.x - Muse);
+        den = fmaf(wgt, ml.y, den);
+        num[0] = fmaf(wgt, ov.x, num[0]);
+        num[1] = fmaf(wgt, ov.y, num[1]);
+        num[2] = fmaf(wgt, ov.z, num[2]);
+        num[3] = fmaf(wgt, ov.w, num[3]);
     }
     const int64_t q = r % Lq, h = (r / Lq) % H, b = r / (Lq * H);
-    out[b * os0 + q * os1 + h * os2 + d] = (uint16_t)f32_to_bf16_bits(den > 0.0f ? num / den : 0.0f);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16_bits(den > 0.0f ? num[e] / den : 0.0f);
+    *reinterpret_cast<uint2*>(out + b * os0 + q * os1 + h * os2 + d) =
+        make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
 }
 
 }  // namespace attn
@@ -957,8 +974,8 @@ static int launch_rows(attn::Params p, int64_t B, int64_t row0, int64_t rows, in
     if (rc != HN_OK || sp <= 1) return rc;
     const int64_t nrows = B * p.H * rows;
     HN_REQUIRE(nrows <= 0x7fffffffLL, HN_E_ARG, "hn_attn_fp8kv: too many rows to combine");
-    attn::attn_combine_kernel<<<(unsigned)nrows, attn::D, 0, stream>>>(p.ws_o, p.ws_ml, sp, nrows, rows, p.H,
-                                                                       p.out, p.os0, p.os1, p.os2);
+    attn::attn_combine_kernel<<<(unsigned)((nrows + attn::COMBINE_ROWS - 1) / attn::COMBINE_ROWS), 256, 0, stream>>>(
+        p.ws_o, p.ws_ml, sp, nrows, rows, p.H, p.out, p.os0, p.os1, p.os2);
     return check_launch("hn_attn_fp8kv (combine)");
 }
 
