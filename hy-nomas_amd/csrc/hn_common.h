@@ -165,6 +165,17 @@ HN_DEVICE float group_max(float v) {
     return v;
 }
 
+// The maximum that propagates NaN (IEEE maximum; v_maximum3_f32 on gfx950),
+// as torch's amax does: the activation quantizers' row and block maxima.
+HN_DEVICE float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+template <int WIDTH>
+HN_DEVICE float group_max_nan(float v) {
+#pragma unroll
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v = max_nan(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
 template <int WIDTH>
 HN_DEVICE float group_sum(float v) {
 #pragma unroll

@@ -54,13 +54,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
             const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
-                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+                amax = max_nan(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+                amax = max_nan(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
             }
         }
     }
-    amax = group_max<64>(amax);
-    const float s = mode == HN_SCALE_CLAMP ? fmaxf(amax, amax_floor) / kE4M3Max
+    amax = group_max_nan<64>(amax);
+    const float s = mode == HN_SCALE_CLAMP ? max_nan(amax, amax_floor) / kE4M3Max
                                            : (amax > 0.0f ? amax / kE4M3Max : 1.0f);
     if (lane == 0) scale[row] = s;
     const Quot d(s);
@@ -103,15 +103,16 @@ __global__ __launch_bounds__(256) void quantize_rows_wide_kernel(
             if (c < nchunks) {
                 const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
+                for (int j = 0; j < 4; ++j)
+                    amax = max_nan(amax, max_nan(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
             }
         }
-        amax = group_max<64>(amax);
+        amax = group_max_nan<64>(amax);
         if (lane == 0) wave_max[wave] = amax;
         __syncthreads();
-        amax = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+        amax = max_nan(max_nan(wave_max[0], wave_max[1]), max_nan(wave_max[2], wave_max[3]));
         __syncthreads();  // wave_max is rewritten for the next row
-        const float s = mode == HN_SCALE_CLAMP ? fmaxf(amax, amax_floor) / kE4M3Max
+        const float s = mode == HN_SCALE_CLAMP ? max_nan(amax, amax_floor) / kE4M3Max
                                                : (amax > 0.0f ? amax / kE4M3Max : 1.0f);
         if (t == 0) scale[row] = s;
         const Quot d(s);
@@ -225,13 +226,13 @@ __global__ __launch_bounds__(256) void ln_mod_quantize_kernel(
                     const uint32_t a = f32x2_to_bf16x2(1.0f + bf16_lo(ws[j]), 1.0f + bf16_hi(ws[j]));
                     const uint32_t m = f32x2_to_bf16x2(bf16_lo(y) * bf16_lo(a), bf16_hi(y) * bf16_hi(a));
                     w[j] = f32x2_to_bf16x2(bf16_lo(m) + bf16_lo(wh[j]), bf16_hi(m) + bf16_hi(wh[j]));
-                    amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
+                    amax = max_nan(amax, max_nan(fabsf(bf16_lo(w[j])), fabsf(bf16_hi(w[j]))));
                 }
                 v[i] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
-        amax = group_max<64>(amax);
-        const float s = fmaxf(amax, amax_floor) / kE4M3Max;
+        amax = group_max_nan<64>(amax);
+        const float s = max_nan(amax, amax_floor) / kE4M3Max;
         if (lane == 0) scale[row] = s;
         const Quot d(s);
         uint8_t* qr = q + row * cols;
@@ -266,17 +267,17 @@ __global__ __launch_bounds__(256) void quantize_blockwise_kernel(
             const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
-                amax = fmaxf(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
+                amax = max_nan(amax, fabsf(bf16_bits_to_f32(w[j] & 0xffffu)));
+                amax = max_nan(amax, fabsf(bf16_bits_to_f32(w[j] >> 16)));
             }
         }
     }
-    amax = group_max<64>(amax);
+    amax = group_max_nan<64>(amax);
     __shared__ float red[4];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float s = fmaxf(amax, 1e-4f) / kE4M3Max;
+    amax = max_nan(max_nan(red[0], red[1]), max_nan(red[2], red[3]));
+    const float s = max_nan(amax, 1e-4f) / kE4M3Max;
     if (threadIdx.x == 0) scale[blockIdx.x * gridDim.y + blockIdx.y] = s;
     const Quot d(s);
     d.with_form([&](auto form) {

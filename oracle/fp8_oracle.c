@@ -94,7 +94,11 @@ void hn_oracle_e4m3_decode_n(const uint8_t *q, int64_t n, float *y)
  *      used for linear activations (per token) and weights (per channel).
  *  mode 1 ("zero-one"): s = amax > 0 ? amax / 448 : 1
  *      int8_kv_cache.py:44,152 `where(peak > 0, peak / 127.0, 1.0)` with the
- *      e4m3 range 448 in place of 127; used for K/V rows. */
+ *      e4m3 range 448 in place of 127; used for K/V rows.
+ *  A NaN element makes the row / block amax NaN (torch's amax propagates it):
+ *  in mode 0 the scale is then NaN (clamp_min keeps NaN) and every code of
+ *  the row is a NaN code; in mode 1 the comparison is false and the scale is
+ *  1. (The KV API rejects non-finite rows before they get here.) */
 static inline float fp8_scale(float amax, int mode, float floor_)
 {
     if (mode == 0)
@@ -114,7 +118,7 @@ void hn_oracle_quantize_rows_fp8(const uint16_t *x, int64_t rows, int64_t cols,
         float amax = 0.0f;
         for (int64_t c = 0; c < cols; ++c) {
             const float v = fabsf(bf16_to_f32(xr[c]));
-            amax = v > amax ? v : amax;
+            amax = (v > amax || v != v) ? v : amax;   /* NaN propagates, as torch's amax */
         }
         const float s = fp8_scale(amax, mode, floor_);
         scale[r] = s;
@@ -137,7 +141,7 @@ void hn_oracle_quantize_blockwise_fp8(const uint16_t *x, int64_t rows, int64_t c
             for (int64_t r = bi * 128; r < rows && r < bi * 128 + 128; ++r)
                 for (int64_t c = bj * 128; c < bj * 128 + 128; ++c) {
                     const float v = fabsf(bf16_to_f32(x[r * cols + c]));
-                    amax = v > amax ? v : amax;
+                    amax = (v > amax || v != v) ? v : amax;   /* NaN propagates */
                 }
             const float s = fp8_scale(amax, 0, 1e-4f);
             scale[bi * kb + bj] = s;

@@ -239,3 +239,46 @@ def test_ln_modulate_quantize_rejects_bad_shapes(dev):
         ops.ln_modulate_quantize_fp8(x, sh[:, :32], sc, 1e-6)
     with pytest.raises(TypeError):
         ops.ln_modulate_quantize_fp8(x.float(), sh, sc, 1e-6)
+
+
+def _codes_match(got, want):
+    """Codes equal, except that a NaN code (0x7F | sign) matches either sign:
+    the sign of a NaN after a division is not reproducible across devices."""
+    nan = (want & 0x7F) == 0x7F
+    return np.array_equal(got[~nan], want[~nan]) and ((got[nan] & 0x7F) == 0x7F).all()
+
+
+@pytest.mark.parametrize("cols", [3072, 12288])
+def test_quantizers_non_finite_rows(O, dev, cols):
+    """NaN in a row makes its scale NaN and every code a NaN code (torch's amax
+    propagates NaN; clamp_min keeps it); an infinite row max gives scale inf.
+    Per-token quant in both scale modes (one wave per row for 3072 columns,
+    one workgroup per row for 12288), blockwise quant, and the fused LayerNorm
+    + modulate + quant, against the oracle."""
+    print(f"case non-finite rows cols={cols}", flush=True)
+    ops = pkg_module("ops")
+    x = _gen((24, cols), 5, 2.0)
+    x[3, 17] = float("nan")
+    x[7, :] = float("nan")
+    x[11, 40] = float("inf")
+    x[15, 41] = -float("inf")
+    bits = bf16_bits(x)
+    for mode in (0, 1):
+        q, s = ops.quantize_rows_fp8(x.to(dev), mode, 1e-4)
+        qo, so = O.quantize_rows_fp8(bits, mode)
+        assert np.array_equal(s.cpu().numpy(), so, equal_nan=True), mode
+        assert _codes_match(u8(q), qo), mode
+    if cols % 128 == 0:
+        xb = torch.cat([x, _gen((104, cols), 6, 2.0)])          # 128 rows: one block row
+        q, s = ops.quantize_blockwise_fp8(xb.to(dev))
+        qo, so = O.quantize_blockwise_fp8(bf16_bits(xb))
+        assert np.isnan(so).any() and np.array_equal(s.cpu().numpy(), so, equal_nan=True)
+        assert _codes_match(u8(q), qo)
+    if cols <= 8192:
+        sh = (torch.randn(1, cols) * 0.5).to(torch.bfloat16)
+        sc = (torch.randn(1, cols) * 0.5).to(torch.bfloat16)
+        q, s = ops.ln_modulate_quantize_fp8(x.view(1, 24, cols).to(dev), sh.to(dev), sc.to(dev), 1e-6)
+        qo, so = O.ln_modulate_quantize_fp8(bits, bf16_bits(sh), bf16_bits(sc), 1e-6, rows_per_batch=24)
+        assert np.isnan(so[[3, 7, 11, 15]]).all()
+        assert np.array_equal(s.cpu().numpy(), so, equal_nan=True)
+        assert _codes_match(u8(q), qo)

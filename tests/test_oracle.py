@@ -117,16 +117,24 @@ def test_row_quant_matches_torch_reference_recipe(O):
     rng = np.random.default_rng(3)
     x = torch.from_numpy(rng.standard_normal((64, 3072)).astype(np.float32)).to(torch.bfloat16)
     x[rng.random((64, 3072)) < 0.001] *= 20
+    # non-finite rows: torch's amax propagates NaN (NaN scale, NaN codes) and
+    # an infinite row max gives scale inf (codes of x / inf)
+    x[5, 100] = float("nan")
+    x[9, 3] = float("inf")
+    x[11, 7] = -float("inf")
+    x[13, :] = float("nan")
     xf = x.float()
     s_lin = xf.abs().amax(dim=1, keepdim=True).clamp_min(1e-4) / 448.0
     q_lin = (xf / s_lin).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     q, s = O.quantize_rows_fp8(bf16_bits(x), O.SCALE_CLAMP)
-    assert np.array_equal(q, q_lin) and np.array_equal(s, s_lin.numpy()[:, 0])
+    assert np.isnan(s[5]) and np.isnan(s[13]) and np.isinf(s[9]) and np.isinf(s[11])
+    assert np.array_equal(q, q_lin) and np.array_equal(s, s_lin.numpy()[:, 0], equal_nan=True)
     peak = xf.abs().amax(dim=1, keepdim=True)
     s_kv = torch.where(peak > 0, peak / 448.0, torch.ones_like(peak))
     q_kv = (xf / s_kv).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     q, s = O.quantize_rows_fp8(bf16_bits(x), O.SCALE_ZERO_ONE)
-    assert np.array_equal(q, q_kv) and np.array_equal(s, s_kv.numpy()[:, 0])
+    assert s[5] == 1.0 and s[13] == 1.0                   # NaN > 0 is false: the "else 1" branch
+    assert np.array_equal(q, q_kv) and np.array_equal(s, s_kv.numpy()[:, 0], equal_nan=True)
 
 
 # ------------------------------------------------ LayerNorm + adaLN modulate
@@ -211,14 +219,16 @@ def test_blockwise_quant_known_answers_and_padding(O):
 def test_blockwise_quant_matches_torch_reference_recipe(O):
     rng = np.random.default_rng(4)
     x = torch.from_numpy(rng.standard_normal((300, 384)).astype(np.float32)).to(torch.bfloat16)
+    x[140, 200] = float("nan")                            # block (1, 1): NaN scale, NaN codes
     m, k = x.shape
     padded = torch.nn.functional.pad(x, (0, 0, 0, (-m) % 128))
     blocks = padded.float().reshape(-1, 128, k // 128, 128)
     scale = blocks.abs().amax(dim=(1, 3)).clamp_min(1e-4) / 448.0
     qt = (blocks / scale[:, None, :, None]).to(torch.float8_e4m3fn).reshape(-1, k)[:m]
     q, s = O.quantize_blockwise_fp8(bf16_bits(x))
+    assert np.isnan(s[1, 1]) and np.isfinite(np.delete(s.ravel(), 1 * s.shape[1] + 1)).all()
     assert np.array_equal(q, qt.view(torch.uint8).numpy())
-    assert np.array_equal(s, scale.numpy())
+    assert np.array_equal(s, scale.numpy(), equal_nan=True)
 
 
 # ---------------------------------------------------------------- KV cache
