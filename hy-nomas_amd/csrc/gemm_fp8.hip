@@ -61,6 +61,10 @@ struct Params {
     // (the last row stripe if M % 256 != 0, then the last column stripe if
     // N % 256 != 0); each class is split evenly over the 8 XCDs.
     int tm_full, tn_full, tiles_full, tiles_part, m_tail;
+    // Tile width in columns: 256, except in the persistent row/column kernel,
+    // which takes 192 when a launch has fewer 256-wide tiles than CUs and
+    // more, still at most one per CU, at 192 (its WC template argument).
+    int bn;
 };
 
 // 16-byte chunk c of LDS row r lives at chunk position c ^ ((r >> 1) & 7).
@@ -734,17 +738,18 @@ HN_DEVICE void dma_4B_sbase(const void* sbase, uint32_t voff, uint32_t lds) {
 // Parameter DMA q (0..4) of a wave's sub-tile, 256 bytes each: row scales at
 // [0, 512), column scales at [512, 1024), bias pairs at [1024, 1280). Indices
 // are clamped to the operand's end (in bounds; never used).
+template <int WC>
 HN_DEVICE void param_dma(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane, uint32_t lds, int q) {
     if (q < 2) {
         int64_t m = m0 + wm * 128 + 64 * q + lane;
         m = m < p.M ? m : p.M - 1;
         dma_4B_sbase(p.sa, (uint32_t)(m * 4), lds + 256 * q);
     } else if (q < 4) {
-        int64_t n = n0 + wn * 128 + 64 * (q - 2) + lane;
+        int64_t n = n0 + wn * WC + 64 * (q - 2) + lane;
         n = n < p.N ? n : p.N - 1;
         dma_4B_sbase(p.sb, (uint32_t)(n * 4), lds + 512 + 256 * (q - 2));
     } else if (p.bias) {
-        int64_t n = n0 + wn * 128 + 2 * lane;
+        int64_t n = n0 + wn * WC + 2 * lane;
         n = n < p.N ? n : p.N - 2;
         dma_4B_sbase(p.bias, (uint32_t)(n * 2), lds + 1024);
     } else {
@@ -818,18 +823,20 @@ HN_DEVICE uint4 oe_readback(const uint8_t* stg, int q, int lane) {
     return *reinterpret_cast<const uint4*>(stg + rr * 128 + ((c ^ ((rr >> 1) & 7)) << 4));
 }
 
+template <int WC>
 HN_DEVICE void oe_store(const Params& p, int64_t pm0, int64_t pn0, int wm, int wn, int P, int q, const uint4& v,
                         int lane) {
     const int j = P >> 1, ih = P & 1;
     const int rr = 8 * q + (lane >> 3), c = lane & 7;
     const int64_t m = pm0 + wm * 128 + 32 * j + rr;
-    const int64_t n = pn0 + wn * 128 + 64 * ih + 8 * c;
-    if (m < p.M && n < p.N) *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) = v;
+    const int nl = 64 * ih + 8 * c;  // column within the wave's wc columns
+    const int64_t n = pn0 + wn * WC + nl;
+    if (m < p.M && n < p.N && (WC == 128 || nl < WC)) *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) = v;
 }
 
 // All eight passes of a pending tile without overlap (before an edge tile and
 // after a workgroup's last tile).
-template <int ACT>
+template <int ACT, int WC>
 HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, int64_t pm0, int64_t pn0,
                         int wm, int wn, int lane) {
 #pragma unroll
@@ -840,7 +847,7 @@ HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, i
 #pragma unroll
         for (int g = 0; g < 8; ++g) oe_write(y, stg, P, g, lane);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) oe_store(p, pm0, pn0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
+        for (int q = 0; q < 4; ++q) oe_store<WC>(p, pm0, pn0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
     }
 }
 
@@ -850,7 +857,7 @@ HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, i
 // bytes, without the LDS staging of the carried passes: the 8 stores of a
 // pass write every byte of its 32 rows' 128-byte lines, which the L2 merges.
 // (Measured with bias + GELU: 387 against 393 us through the staging area.)
-template <int ACT>
+template <int ACT, int WC>
 HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, int64_t m0,
                              int64_t n0, int wm, int wn, int lane) {
     const int h = lane >> 5, r = lane & 31;
@@ -870,6 +877,7 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
 #pragma unroll
             for (int vq = 0; vq < 4; ++vq) {
                 const int i = 2 * ih + ii, nl = 32 * i + 8 * vq + 4 * h;
+                if (32 * i >= WC) continue;  // block past a 96-column wave
                 const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
                 const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
                 float v[4] = {fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bf16_bits_to_f32(bb.x & 0xffffu)),
@@ -886,14 +894,17 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
                     o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
                 }
                 const int64_t m = m0 + wm * 128 + 32 * j + r;
-                const int64_t n = n0 + wn * 128 + nl;
+                const int64_t n = n0 + wn * WC + nl;
                 if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
             }
     }
 }
 
-template <int ACT>
+// WC: columns per wave, 128 (256 x 256 tiles) or 96 (256 x 192 tiles, which
+// take the edge-tile path: no carried epilogue).
+template <int ACT, int WC>
 __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
+    constexpr int TBN = 2 * WC;  // tile columns
     __shared__ __attribute__((aligned(16))) uint8_t smem[O_SMEM];
     const int xcd = blockIdx.x & 7;
     const int stride = (int)(gridDim.x >> 3);  // workgroups per XCD
@@ -920,11 +931,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     const uint8_t* b_src = nullptr;
     int a_last = 0, b_last = 0;  // last valid row of the source tile, tile-relative
     auto set_src = [&](int tm_, int tn_) {
-        const int64_t m0_ = (int64_t)tm_ * BM, n0_ = (int64_t)tn_ * BN;
+        const int64_t m0_ = (int64_t)tm_ * BM, n0_ = (int64_t)tn_ * TBN;
         a_src = p.a + m0_ * p.K;
         b_src = p.b + n0_ * p.K;
         a_last = (int)((p.M - m0_ < BM ? p.M - m0_ : BM) - 1);
-        b_last = (int)((p.N - n0_ < BN ? p.N - n0_ : BN) - 1);
+        // A 192-wide tile still fills all 256 stage rows: rows past its width
+        // repeat its last row (never read by an MFMA).
+        b_last = (int)((p.N - n0_ < TBN ? p.N - n0_ : TBN) - 1);
     };
     // Per-lane DMA geometry from a regenerated lane id l: the lane's row in
     // load 0 and its chunk offsets for even and odd loads.
@@ -943,16 +956,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         const int row = min(d.row + 8 * q, last);
         return (uint32_t)row * (uint32_t)p.K + d.chunk[q & 1];
     };
-    // Current tile: origin and blocks inside the matrix (imax weight blocks,
-    // 0 or 4 as N % 128 == 0; jmax activation blocks of 32 rows). Wave-uniform.
+    // Current tile: origin and blocks inside the matrix (imax weight blocks of
+    // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
+    // 32 rows). Wave-uniform. Tiles with every block inside the matrix take
+    // the carried path.
     int64_t cm0 = 0, cn0 = 0;
     int cimax = 0, cjmax = 0;
     auto set_cur = [&](int tm_, int tn_) {
         cm0 = (int64_t)tm_ * BM;
-        cn0 = (int64_t)tn_ * BN;
-        const int64_t rows_w = p.M - (cm0 + wm * 128), cols_w = p.N - (cn0 + wn * 128);
+        cn0 = (int64_t)tn_ * TBN;
+        const int64_t rows_w = p.M - (cm0 + wm * 128), cols_w = p.N - (cn0 + wn * WC);
         cjmax = rows_w >= 128 ? 4 : (rows_w <= 0 ? 0 : (int)((rows_w + 31) >> 5));
-        cimax = cols_w >= 128 ? 4 : (cols_w <= 0 ? 0 : (int)(cols_w >> 5));
+        cimax = cols_w >= WC ? WC / 32 : (cols_w <= 0 ? 0 : (int)(cols_w >> 5));
     };
     int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
     auto pair_of = [&](int s) { return (s + par) & 1; };
@@ -1000,13 +1015,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         fa[j] = frag_at(buf, wm * 128 + j * 32, kh, d);
     };
     auto read_b = [&](const uint8_t* buf, int i, int kh, const RdLane& d) {
-        fb[i] = frag_at(buf, wn * 128 + i * 32, kh, d);
+        fb[i] = frag_at(buf, wn * WC + i * 32, kh, d);
     };
     // Rolling reads of the next slice after slot s's MFMA.
     auto roll = [&](int s, const uint8_t* abuf, const uint8_t* bbuf, int kh, const RdLane& d) {
         if (s == 3 || s == 7 || s == 11) read_b(bbuf, s >> 2, kh, d);
         if (s >= 12) read_a(abuf, s - 12, kh, d);
-        if (s == 15) read_b(bbuf, 3, kh, d);
+        if (s == 15 && WC == 128) read_b(bbuf, 3, kh, d);  // no fourth block at 96 columns
     };
 
     // One K step. EDGE: edge tile (blocks outside the matrix skipped). PASS:
@@ -1036,7 +1051,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const int i = s >> 2, j = s & 3;
-            if (!EDGE || (i < cimax && j < cjmax)) {
+            if (i < WC / 32 && (!EDGE || (i < cimax && j < cjmax))) {
                 if (FIRST) acc[i][j] = mfma(fb[i], fa[j], f32x16{});
                 else acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
             } else if (FIRST) {
@@ -1055,9 +1070,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             // Read-back of the previous pass (slots 0-3) before this pass's
             // staging writes (slots 3-15), stores two slots after each read.
             if (PASS >= 1 && s < 4) rb[s] = oe_readback(stg, s, el);
-            if (PASS >= 1 && s >= 2 && s < 6) oe_store(p, pm0, pn0, wm, wn, PASS - 1, s - 2, rb[s - 2], el);
+            if (PASS >= 1 && s >= 2 && s < 6) oe_store<WC>(p, pm0, pn0, wm, wn, PASS - 1, s - 2, rb[s - 2], el);
             const int i = s >> 2, j = s & 3;
-            if (!EDGE || (i < cimax && j < cjmax)) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
+            if (i < WC / 32 && (!EDGE || (i < cimax && j < cjmax))) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
             if (NEXT) roll(s, an, bnx, 0, rl);
             if (DMA == 1 || DMA == 3) {
                 if (s < 8) dma_a(dl, k + 2, dst, s);
@@ -1067,7 +1082,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
                 if (s < 8) dma_a(dl, 0, dst, s);
                 else dma_b(dl, 0, dst, s - 8);
             }
-            if (DMA == 3 && s >= 8 && s < 13) param_dma(p, cm0, cn0, wm, wn, el, prm_lds, s - 8);
+            if (DMA == 3 && s >= 8 && s < 13) param_dma<WC>(p, cm0, cn0, wm, wn, el, prm_lds, s - 8);
             if (PASS >= 0 && PASS < O_PASSES) {
                 oe_act<ACT>(y, glo, PASS, 16 + s);
                 if (s >= 4 && s < 8) oe_write(y, stg, PASS, s - 4, el);         // groups 0-3 (half 0)
@@ -1105,11 +1120,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             const RdLane d = rd_lane(fresh_lane());
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                read_b(ab + R_BUF, q, 0, d);
+                if (q < WC / 32) read_b(ab + R_BUF, q, 0, d);
                 read_a(ab, q, 0, d);
             }
         }
-        const bool whole = cimax == 4 && cjmax == 4;
+        const bool whole = cimax == WC / 32 && cjmax == 4;
         if (whole) {
             if (!pending) {
                 // Nothing carried yet: the passes run on zeros, their stores
@@ -1133,7 +1148,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             step(KT - 2, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 2>{}, T{}, F{});
             step(KT - 1, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 0>{}, F{}, F{});
         } else {
-            if (pending) oe_flush<ACT>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+            if (pending) oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
             step(0, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 3>{}, T{}, T{});
             for (int k = 1; k < KT - 2; ++k)
                 step(k, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 1>{}, T{}, F{});
@@ -1152,7 +1167,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
         }
-        direct_passes<ACT>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
+        direct_passes<ACT, WC>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
         convert_tile(acc, y, prm, fresh_lane());
         pm0 = cm0;
         pn0 = cn0;
@@ -1165,7 +1180,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __syncthreads();
     }
-    oe_flush<ACT>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+    oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
     // The last step's re-load of step 0 (no next tile) may still be landing.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -1194,25 +1209,46 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     p.bias = (const uint16_t*)bias;
     p.out = (uint16_t*)out;
     p.M = M; p.N = N; p.K = K; p.ldc = ldc; p.act = act;
-    const int64_t tm = (M + gemm::BM - 1) / gemm::BM, tn = (N + gemm::BN - 1) / gemm::BN;
-    HN_REQUIRE(tm * tn <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
-    p.tiles_m = (int)tm; p.tiles_n = (int)tn;
-    p.per_xcd = (int)((tm * tn + 7) / 8);
-    p.tm_full = (int)(M / gemm::BM);
-    p.tn_full = (int)(N / gemm::BN);
-    p.m_tail = (int)(M % gemm::BM != 0);
-    p.tiles_full = p.tm_full * p.tn_full;
-    p.tiles_part = (int)(tm * tn) - p.tiles_full;
-    if (mode == gemm::ROWCOL) p.per_xcd = (p.tiles_full + 7) / 8 + (p.tiles_part + 7) / 8;
+    const int64_t tm = (M + gemm::BM - 1) / gemm::BM;
+    HN_REQUIRE(tm * ((N + 191) / 192) <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
+    auto set_tiles = [&](int bn) {
+        const int64_t tn = (N + bn - 1) / bn;
+        p.bn = bn;
+        p.tiles_m = (int)tm; p.tiles_n = (int)tn;
+        p.tm_full = (int)(M / gemm::BM);
+        p.tn_full = (int)(N / bn);
+        p.m_tail = (int)(M % gemm::BM != 0);
+        p.tiles_full = p.tm_full * p.tn_full;
+        p.tiles_part = (int)(tm * tn) - p.tiles_full;
+        p.per_xcd = mode == gemm::ROWCOL ? (p.tiles_full + 7) / 8 + (p.tiles_part + 7) / 8 : (int)((tm * tn + 7) / 8);
+    };
+    set_tiles(gemm::BN);
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
     if (mode == gemm::ROWCOL && K / gemm::BK >= gemm::O_MIN_KT) {
         // Persistent: per XCD, min(queue length, CUs of the XCD) workgroups.
-        const int per_xcd_cus = device_cus() / 8 > 0 ? device_cus() / 8 : 1;
+        // A launch of fewer 256-wide tiles than CUs is one round whatever
+        // the tile; 192-wide tiles (three 32-column blocks per wave) do 3/4
+        // of the work each and fill more CUs (config 1, 4096 x 3072: 192 ->
+        // 256 tiles).
+        const int cus = device_cus();
+        const int per_xcd_cus = cus / 8 > 0 ? cus / 8 : 1;
+        const int64_t t256 = tm * ((N + 255) / 256), t192 = tm * ((N + 191) / 192);
+        if (t256 < cus && t192 > t256) {
+            set_tiles(192);
+            if (p.per_xcd > per_xcd_cus) set_tiles(gemm::BN);  // would need a second round
+        }
         const dim3 pgrid((unsigned)(8 * (p.per_xcd < per_xcd_cus ? p.per_xcd : per_xcd_cus)));
-        if (act == HN_ACT_GELU_TANH)
-            gemm::gemm_rowcol_oe_kernel<HN_ACT_GELU_TANH><<<pgrid, gemm::NT, 0, (hipStream_t)stream>>>(p);
-        else
-            gemm::gemm_rowcol_oe_kernel<HN_ACT_NONE><<<pgrid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+        const hipStream_t st = (hipStream_t)stream;
+        if (p.bn == 192) {
+            if (act == HN_ACT_GELU_TANH)
+                gemm::gemm_rowcol_oe_kernel<HN_ACT_GELU_TANH, 96><<<pgrid, gemm::NT, 0, st>>>(p);
+            else
+                gemm::gemm_rowcol_oe_kernel<HN_ACT_NONE, 96><<<pgrid, gemm::NT, 0, st>>>(p);
+        } else if (act == HN_ACT_GELU_TANH) {
+            gemm::gemm_rowcol_oe_kernel<HN_ACT_GELU_TANH, 128><<<pgrid, gemm::NT, 0, st>>>(p);
+        } else {
+            gemm::gemm_rowcol_oe_kernel<HN_ACT_NONE, 128><<<pgrid, gemm::NT, 0, st>>>(p);
+        }
     } else if (mode == gemm::ROWCOL)
         gemm::gemm_rowcol_kernel<<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     else

@@ -86,10 +86,16 @@ def test_linear_fp8_no_bias_and_strided_out(O, dev):
 # epilogue into the next tile's K loop. Cases: the smallest such K and the
 # largest K below it; ragged M and N (edge tiles); more tiles than CUs, so a
 # workgroup walks whole and edge tiles in turn; with and without bias / GELU.
+# A launch with fewer 256-wide tiles than CUs runs 256 x 192 tiles when that
+# gives more tiles and still one round (96 columns per wave): config 1 and
+# (64, 12288, 3072) above, and the 1000 x 640 and 700 x 1280 cases here, whose
+# last column stripes are 64 wide (one wave with two blocks, one with none) and
+# 128 wide (three blocks and one).
 @pytest.mark.parametrize("M,K,N,gelu,bias", [
     (300, 896, 384, True, True),      # smallest K on the carried-epilogue path
     (300, 768, 384, True, True),      # largest K below it
-    (1000, 1280, 640, True, True),    # M and N edges, 12 tiles
+    (1000, 1280, 640, True, True),    # M and N edges, 256 x 192 tiles (16)
+    (700, 1024, 1280, True, False),   # 256 x 192 tiles (21), both edges, no bias
     (4700, 1024, 4224, True, False),  # 323 tiles: two per workgroup, both edges, no bias
     (4700, 1024, 4224, False, True),
 ])
