@@ -105,21 +105,25 @@ def test_linear_fp8_persistent_tiles(O, dev, M, K, N, gelu, bias):
     _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
 
 
-def test_gemm_rowcol_persistent_strided_out(dev):
-    """ldc > N on the carried-epilogue path (K = 1024): columns past N untouched."""
+@pytest.mark.parametrize("N", [384, 640])
+def test_gemm_rowcol_persistent_strided_out(dev, N):
+    """ldc > N on the carried-epilogue path (K = 1024): columns past N untouched.
+    N = 384 runs 256-wide tiles; N = 640 runs 256 x 192 tiles with a 64-wide
+    last stripe, whose 96-column waves must not write past their own columns."""
     ops = pkg_module("ops")
     L = pkg_module("_lib")
+    ldc = N + 8
     a = torch.randint(0, 120, (300, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
-    b = torch.randint(0, 120, (384, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (N, 1024), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
     sa = torch.rand(300, device=dev) + 0.5
-    sb = torch.rand(384, device=dev) + 0.5
-    out = torch.full((300, 392), 3.0, dtype=torch.bfloat16, device=dev)
+    sb = torch.rand(N, device=dev) + 0.5
+    out = torch.full((300, ldc), 3.0, dtype=torch.bfloat16, device=dev)
     L.check(L.load().hn_gemm_fp8_rowcol(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(),
-                                        None, out.data_ptr(), 300, 384, 1024, 392, 0,
+                                        None, out.data_ptr(), 300, N, 1024, ldc, 0,
                                         torch.cuda.current_stream().cuda_stream), "gemm")
     ref = ops.gemm_fp8_rowcol(a, b, sa, sb)
-    assert torch.equal(out[:, :384], ref)
-    assert (out[:, 384:] == 3.0).all()
+    assert torch.equal(out[:, :N], ref)
+    assert (out[:, N:] == 3.0).all()
 
 
 def test_gemm_rowcol_is_deterministic(dev):
