@@ -944,17 +944,26 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     struct DmaLane {
         int row;
         uint32_t chunk[2];
+        uint32_t rowk;  // row * K
     };
     auto dma_lane = [&](int l) {
         DmaLane d;
         d.row = wave * 64 + (l >> 3);
         d.chunk[0] = (uint32_t)swz_pos(d.row, l & 7) << 4;
         d.chunk[1] = (uint32_t)swz_pos(d.row + 8, l & 7) << 4;
+        d.rowk = (uint32_t)d.row * (uint32_t)p.K;
         return d;
     };
-    auto dma_off = [&](const DmaLane& d, int q, int last) {
-        const int row = min(d.row + 8 * q, last);
-        return (uint32_t)row * (uint32_t)p.K + d.chunk[q & 1];
+    // CLAMP (edge tiles, the next tile's loads, 192-wide B): rows past the
+    // source's last row read that row. Without it the offset is row K +
+    // chunk + 8 q K with 8 q K wave-uniform: one add per load instead of a
+    // clamp and a 64-bit multiply-add.
+    auto dma_off = [&](const DmaLane& d, int q, int last, bool clamp) {
+        if (clamp) {
+            const int row = min(d.row + 8 * q, last);
+            return (uint32_t)row * (uint32_t)p.K + d.chunk[q & 1];
+        }
+        return d.rowk + d.chunk[q & 1] + (uint32_t)(8 * q) * (uint32_t)p.K;
     };
     // Current tile: origin and blocks inside the matrix (imax weight blocks of
     // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
@@ -971,11 +980,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     };
     int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
     auto pair_of = [&](int s) { return (s + par) & 1; };
-    auto dma_a = [&](const DmaLane& d, int src_step, int pr, int q) {
-        dma_16B_sbase(a_src + (int64_t)src_step * BK, dma_off(d, q, a_last), lds_base + (2 * pr) * R_BUF + q * 1024);
+    auto dma_a = [&](const DmaLane& d, int src_step, int pr, int q, bool clamp = true) {
+        dma_16B_sbase(a_src + (int64_t)src_step * BK, dma_off(d, q, a_last, clamp),
+                      lds_base + (2 * pr) * R_BUF + q * 1024);
     };
-    auto dma_b = [&](const DmaLane& d, int src_step, int pr, int q) {
-        dma_16B_sbase(b_src + (int64_t)src_step * BK, dma_off(d, q, b_last),
+    auto dma_b = [&](const DmaLane& d, int src_step, int pr, int q, bool clamp = true) {
+        dma_16B_sbase(b_src + (int64_t)src_step * BK, dma_off(d, q, b_last, clamp),
                       lds_base + (2 * pr + 1) * R_BUF + q * 1024);
     };
 
@@ -1075,8 +1085,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             if (i < WC / 32 && (!EDGE || (i < cimax && j < cjmax))) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
             if (NEXT) roll(s, an, bnx, 0, rl);
             if (DMA == 1 || DMA == 3) {
-                if (s < 8) dma_a(dl, k + 2, dst, s);
-                else dma_b(dl, k + 2, dst, s - 8);
+                // This tile's rows: all inside the operands for a whole tile
+                // (B of a 192-wide tile still clamps rows 192-255).
+                if (s < 8) dma_a(dl, k + 2, dst, s, EDGE);
+                else dma_b(dl, k + 2, dst, s - 8, EDGE || WC < 128);
             }
             if (DMA == 2) {
                 if (s < 8) dma_a(dl, 0, dst, s);
