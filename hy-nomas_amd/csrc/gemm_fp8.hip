@@ -929,18 +929,23 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     // depends only on q % 2 (chunk[q & 1]).
     const uint8_t* a_src = nullptr;
     const uint8_t* b_src = nullptr;
-    int a_last = 0, b_last = 0;  // last valid row of the source tile, tile-relative
+    // Largest offset a load may take from its K step's source address
+    // (src + 128 step): the last 16-byte chunk of the step's 128-byte window
+    // of the source tile's last row inside the operand, last K + 112.
+    uint32_t a_lim = 0, b_lim = 0;
     auto set_src = [&](int tm_, int tn_) {
         const int64_t m0_ = (int64_t)tm_ * BM, n0_ = (int64_t)tn_ * TBN;
         a_src = p.a + m0_ * p.K;
         b_src = p.b + n0_ * p.K;
-        a_last = (int)((p.M - m0_ < BM ? p.M - m0_ : BM) - 1);
-        // A 192-wide tile still fills all 256 stage rows: rows past its width
-        // repeat its last row (never read by an MFMA).
-        b_last = (int)((p.N - n0_ < TBN ? p.N - n0_ : TBN) - 1);
+        const int64_t a_rows = p.M - m0_ < BM ? p.M - m0_ : BM;
+        // A 192-wide tile still fills all 256 stage rows; rows past its width
+        // are clamped like rows past N (never read by an MFMA).
+        const int64_t b_rows = p.N - n0_ < TBN ? p.N - n0_ : TBN;
+        a_lim = (uint32_t)((a_rows - 1) * p.K + 112);
+        b_lim = (uint32_t)((b_rows - 1) * p.K + 112);
     };
     // Per-lane DMA geometry from a regenerated lane id l: the lane's row in
-    // load 0 and its chunk offsets for even and odd loads.
+    // load 0, its chunk offsets for even and odd loads, and row K.
     struct DmaLane {
         int row;
         uint32_t chunk[2];
@@ -954,16 +959,15 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         d.rowk = (uint32_t)d.row * (uint32_t)p.K;
         return d;
     };
-    // CLAMP (edge tiles, the next tile's loads, 192-wide B): rows past the
-    // source's last row read that row. Without it the offset is row K +
-    // chunk + 8 q K with 8 q K wave-uniform: one add per load instead of a
-    // clamp and a 64-bit multiply-add.
-    auto dma_off = [&](const DmaLane& d, int q, int last, bool clamp) {
-        if (clamp) {
-            const int row = min(d.row + 8 * q, last);
-            return (uint32_t)row * (uint32_t)p.K + d.chunk[q & 1];
-        }
-        return d.rowk + d.chunk[q & 1] + (uint32_t)(8 * q) * (uint32_t)p.K;
+    // Offset of load q: row K + chunk + 8 q K (8 q K wave-uniform), capped
+    // at the source tile's limit. A row r <= last keeps its offset
+    // (r K + chunk <= last K + 112, chunk <= 112); a row past the operand's
+    // end starts at >= (last + 1) K >= last K + 128 and reads the last
+    // chunk of the last row's window instead (never used). Every load of
+    // every wave stays inside the operand, whichever rows the wave itself
+    // multiplies.
+    auto dma_off = [&](const DmaLane& d, int q, uint32_t lim) {
+        return min(d.rowk + d.chunk[q & 1] + (uint32_t)(8 * q) * (uint32_t)p.K, lim);
     };
     // Current tile: origin and blocks inside the matrix (imax weight blocks of
     // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
@@ -980,12 +984,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     };
     int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
     auto pair_of = [&](int s) { return (s + par) & 1; };
-    auto dma_a = [&](const DmaLane& d, int src_step, int pr, int q, bool clamp = true) {
-        dma_16B_sbase(a_src + (int64_t)src_step * BK, dma_off(d, q, a_last, clamp),
-                      lds_base + (2 * pr) * R_BUF + q * 1024);
+    auto dma_a = [&](const DmaLane& d, int src_step, int pr, int q) {
+        dma_16B_sbase(a_src + (int64_t)src_step * BK, dma_off(d, q, a_lim), lds_base + (2 * pr) * R_BUF + q * 1024);
     };
-    auto dma_b = [&](const DmaLane& d, int src_step, int pr, int q, bool clamp = true) {
-        dma_16B_sbase(b_src + (int64_t)src_step * BK, dma_off(d, q, b_last, clamp),
+    auto dma_b = [&](const DmaLane& d, int src_step, int pr, int q) {
+        dma_16B_sbase(b_src + (int64_t)src_step * BK, dma_off(d, q, b_lim),
                       lds_base + (2 * pr + 1) * R_BUF + q * 1024);
     };
 
@@ -1085,10 +1088,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             if (i < WC / 32 && (!EDGE || (i < cimax && j < cjmax))) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
             if (NEXT) roll(s, an, bnx, 0, rl);
             if (DMA == 1 || DMA == 3) {
-                // This tile's rows: all inside the operands for a whole tile
-                // (B of a 192-wide tile still clamps rows 192-255).
-                if (s < 8) dma_a(dl, k + 2, dst, s, EDGE);
-                else dma_b(dl, k + 2, dst, s - 8, EDGE || WC < 128);
+                if (s < 8) dma_a(dl, k + 2, dst, s);
+                else dma_b(dl, k + 2, dst, s - 8);
             }
             if (DMA == 2) {
                 if (s < 8) dma_a(dl, 0, dst, s);

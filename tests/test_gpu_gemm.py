@@ -98,10 +98,15 @@ def test_linear_fp8_no_bias_and_strided_out(O, dev):
     (700, 1024, 1280, True, False),   # 256 x 192 tiles (21), both edges, no bias
     (4700, 1024, 4224, True, False),  # 323 tiles: two per workgroup, both edges, no bias
     (4700, 1024, 4224, False, True),
+    # Last row tile 132 deep: waves of rows 0-127 multiply a whole block while
+    # the stage rows they load (128-191) lie partly past M; the loads must
+    # stay inside A. On 256 x 192 tiles, and on 256-wide ones (340 tiles).
+    (132, 12288, 3072, True, True),
+    (4996, 1024, 4224, False, True),
 ])
 def test_linear_fp8_persistent_tiles(O, dev, M, K, N, gelu, bias):
     print(f"case linear persistent {M}x{K}x{N} gelu={gelu} bias={bias}", flush=True)
-    rows = None if M <= 1000 else np.concatenate([np.arange(0, 64), np.arange(2300, 2364), np.arange(4400, 4700)])
+    rows = None if M <= 1000 else np.concatenate([np.arange(0, 64), np.arange(2300, 2364), np.arange(M - 300, M)])
     _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
 
 
