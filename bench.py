@@ -171,7 +171,7 @@ def main():
     kv_args = (L.HN_KV_FP8, kt.data_ptr(), vt.data_ptr(), L.strides(kt), 1, KV_L, KV_H, KV_D,
                cache["k"].data_ptr(), cache["v"].data_ptr(), L.strides(cache["k"]),
                cache["k_scale"].data_ptr(), cache["v_scale"].data_ptr(), L.strides(cache["k_scale"]),
-               slot, stream_ptr)
+               cache["k"].shape[1], slot, None, stream_ptr)
     L.check(lib.hn_kv_quantize_pair(*kv_args), "hn_kv_quantize_pair")
     ms_kv = time_loop(lambda: lib.hn_kv_quantize_pair(*kv_args), args.steps, args.warmup)
     kv_gbs = kv_write_bytes() / (ms_kv * 1e-3) / 1e9

@@ -13,6 +13,10 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libhynomas_fp8.so"
 
 HN_OK = 0
+HN_E_ARG = -1
+HN_E_LAUNCH = -2
+HN_E_DEVICE = -3
+ABI_VERSION = 4
 HN_SCALE_CLAMP = 0
 HN_SCALE_ZERO_ONE = 1
 HN_KV_FP8 = 0
@@ -33,17 +37,19 @@ SIGNATURES = {
     "hn_quantize_rows_fp8": [_P, _I64, _I64, _I64, _I, _F, _P, _P, _P],
     "hn_quantize_blockwise_fp8": [_P, _I64, _I64, _P, _P, _P],
     "hn_ln_mod_quantize_fp8": [_P, _I64, _I64, _I64, _P, _P, _I64, _F, _F, _P, _P, _P],
-    "hn_kv_quantize": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _PI64, _P, _PI64, _I64, _P],
+    "hn_kv_quantize": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _PI64, _P, _PI64, _I64, _I64,
+                       _P, _P],
     "hn_kv_quantize_pair": [_I, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P,
-                            _PI64, _I64, _P],
+                            _PI64, _I64, _I64, _P, _P],
     "hn_kv_dequantize": [_I, _P, _PI64, _P, _PI64, _I64, _I64, _I64, _I64, _P, _PI64, _P],
     "hn_gemm_fp8_rowcol": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P],
     "hn_gemm_fp8_blockwise": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "hn_attn_fp8kv": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P, _PI64,
-                      _I64, _P, _P, _PI64, _I64, _I64, _I64, _F, _P, _PI64, _P, _I64, _P],
+                      _I64, _I64, _P, _I64, _P, _P, _PI64, _I64, _P, _I64, _I64, _I64, _F, _P,
+                      _PI64, _P, _I64, _P],
     "hn_attn_fp8kv_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
     "hn_qk_norm_rope_kv": [_I, _P, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _F,
-                           _P, _P, _PI64, _P, _P, _PI64, _I64, _P],
+                           _P, _P, _PI64, _P, _P, _PI64, _I64, _I64, _P, _P],
 }
 RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64}
 
@@ -67,6 +73,9 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = RESTYPES.get(name, _I)
+        if lib.hn_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{p.name} has ABI version {lib.hn_abi_version()}, this binding expects "
+                               f"{ABI_VERSION}: rebuild the library")
         _lib = lib
         return lib
 

@@ -7,18 +7,22 @@
 // 4 waves (128 queries, two workgroups per CU) and 8 waves (256 queries, one
 // per CU); both put 2 waves on each SIMD, and the 8-wave shape dequantizes
 // each K/V tile once for twice the queries. Keys stream through LDS in tiles
-// of 64, two stages. Each tile is dequantized once per workgroup as it is written to LDS,
+// of 64. Each tile is dequantized once per workgroup as it is written to LDS,
 // to the reference's own dequantized values: K = bf16(code * k_scale) and
 // V = bf16(code * v_scale) (fp32 product, rounded to nearest even), so the
-// MFMAs consume exactly the bf16 K/V the reference attends over, and no
-// per-key scale is needed in the compute loop. The optional unquantized tail
-// (the current chunk's bf16 K/V) is copied into the same LDS formats.
+// MFMAs consume exactly the K/V the reference attends over, and no per-key
+// scale is needed in the compute loop. The optional unquantized tail (the
+// current chunk's bf16 K/V) is copied into the same LDS formats.
 //
 // Per 32-key block the wave computes S^T = K Q^T with
 // v_mfma_f32_32x32x16_bf16: the MFMA output puts one query per lane column,
 // so the online-softmax max is lane-local plus one exchange with lane ^ 32,
-// and the row sum stays lane-local until the end. P^T is packed to bf16 in
-// registers and is the B operand of O^T += V^T P^T (same MFMA). V is kept
+// and the row sum stays lane-local until the end. P^T is packed to fp16 in
+// registers and is the B operand of O^T += V^T P^T (v_mfma_f32_32x32x16_f16).
+// fp16 probabilities round at 2^-11 relative instead of bf16's 2^-8; V^T is
+// held as the fp16 form of its bf16 value, which is the same number (a bf16
+// value in fp16's normal range is exactly representable; fp16 subnormals
+// round below 2^-24 and magnitudes past 65504 saturate). V is kept
 // transposed in LDS ([dim][key], keys of each 16-key slice in the order of
 // the P^T registers), so each V^T operand is one 16-byte LDS read.
 //
@@ -27,9 +31,11 @@
 // step_b).
 //
 // Mask: key position p is visible to query position r iff p / chunk <= r / chunk
-// (chunk <= 0: all visible). Tiles wholly beyond the last query's chunk are
-// never visited; tiles wholly visible to every query of the workgroup skip
-// the per-element test.
+// (chunk <= 0: all visible), and, in the MASK instantiation, iff the key's
+// validity byte is non-zero (padded text keys, holes in the cached history:
+// the kv_mask of nomas_cpt.py:611-685). Tiles wholly beyond the last query's
+// chunk are never visited; tiles wholly visible to every query of the
+// workgroup skip the per-element test.
 #include "hn_capi_internal.h"
 #include "hn_common.h"
 
@@ -40,7 +46,7 @@ constexpr int D = 128;
 constexpr int BKV = 64;            // keys per tile
 constexpr int QW = 32;             // queries per wave
 constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spread)
-// V^T tile: 128 dim rows of 64 bf16 keys (128 B) padded to 144 B = 9 16-byte
+// V^T tile: 128 dim rows of 64 fp16 keys (128 B) padded to 144 B = 9 16-byte
 // units, so 16 consecutive rows at one column fall in 16 different bank
 // groups (9 is odd). Column unit c of a row holds the 8 keys 16 (c / 2) +
 // 4 (c % 2) + {0..3} and + 8 + {0..3}: the keys lane half c % 2 feeds to the
@@ -48,7 +54,12 @@ constexpr int KROW = D * 2 + 16;   // K tile row: 128 bf16 + 16 B pad (bank spre
 constexpr int VTROW = 144;
 constexpr int K_BYTES = BKV * KROW;
 constexpr int VT_BYTES = D * VTROW;
-constexpr int STAGE = K_BYTES + VT_BYTES;
+// After K and V^T, each stage holds the tile's 64-bit key-validity word (bit
+// j: key j of the tile exists and is valid), written only by the MASK
+// instantiation.
+constexpr int MASK_OFF = K_BYTES + VT_BYTES;
+constexpr int STAGE = K_BYTES + VT_BYTES + 16;
+constexpr uint64_t ALL_KEYS = ~0ull;
 // Per-key scales of a tile in flight ([0, 64) K, [64, 128) V), two buffers.
 constexpr int SB_FLOATS = 2 * BKV;
 // K/V stages in LDS: three for the 8-wave shape (one workgroup per CU), so
@@ -79,8 +90,13 @@ struct Params {
     const uint16_t* kcur;
     const uint16_t* vcur;
     uint16_t* out;
+    // Key-validity bytes (MASK instantiation; null = every key valid): cache
+    // keys kvalid[b * kvs + t], tail keys uvalid[b * uvs + j].
+    const uint8_t* kvalid;
+    const uint8_t* uvalid;
+    int64_t kvs, uvs;
     int64_t qs0, qs1, qs2;
-    int64_t cs0, cs1, cs2;
+    int64_t cs0, cs1, cs2;   // cs0 == 0 (and ss0 == 0): one cache slot read by every batch
     int64_t ss0, ss1, ss2;
     int64_t us0, us1, us2;
     int64_t os0, os1, os2;
@@ -96,6 +112,8 @@ struct Params {
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // ---------------------------------------------------------------------------
 // Dequantization to the reference's bf16 values.
@@ -121,6 +139,23 @@ HN_DEVICE uint32_t pack_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 
+// fp16 bits of fp32 a and b, packed (a low), round to nearest even.
+HN_DEVICE uint32_t pack_f16(float a, float b) {
+    const f32x2 f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+}
+
+// fp16 bits of the two bf16 values of word w (lo, hi), packed (lo low). Exact
+// for bf16 values in fp16's range; round toward zero, so magnitudes past
+// 65504 saturate instead of overflowing.
+HN_DEVICE uint32_t bf16x2_to_f16x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(bf16_lo(w), bf16_hi(w)));
+}
+
+// fp16 bits of bf16(a), bf16(b): the reference's bf16 dequantized values held
+// as fp16 operands of the PV MFMA.
+HN_DEVICE uint32_t pack_f16_of_bf16(float a, float b) { return bf16x2_to_f16x2(pack_bf16(a, b)); }
+
 // ---------------------------------------------------------------------------
 // Tile loads and LDS writes.
 //
@@ -133,6 +168,8 @@ HN_DEVICE uint32_t pack_bf16(float a, float b) {
 // reads 16 keys x 4 VD contiguous bytes.
 // Scales: threads 0-63 load the K scale of key t, threads 64-127 the V scale
 // of key t - 64, into the tile's scale buffer.
+// Validity (MASK): threads 128-191 (wave 2) load the validity byte of key
+// t - 128; the wave's ballot is the tile's validity word.
 
 // Key (0..63) of entry j (0..3) of quad qd.
 HN_DEVICE int quad_key(int qd, int j) {
@@ -155,6 +192,7 @@ struct CacheRegs {
     uint4 k[Shape<NW>::KU];
     uint32_t v[4][Shape<NW>::VD / 4];  // VD codes (dims VD dg ..) of quad key j
     float s;                           // one per-key scale (threads < 128)
+    uint32_t mk;                       // MASK: validity of key t - 128 (wave 2)
 };
 
 // Base addresses of a cache tile: uniform (scalar) pointers; the per-thread
@@ -164,6 +202,7 @@ struct TileBase {
     const uint8_t* v;
     const float* ks;
     const float* vs;
+    const uint8_t* mk;  // validity bytes of the tile's keys, or null (all valid)
 };
 
 HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t first) {
@@ -174,12 +213,13 @@ HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t firs
     tb.v = p.vc + c;
     tb.ks = p.ks + s;
     tb.vs = p.vs + s;
+    tb.mk = p.kvalid ? p.kvalid + b * p.kvs + first : nullptr;
     return tb;
 }
 
 // Keys past the end of a short tile re-read the tile's last key (they are
 // masked out of the softmax).
-template <int NW>
+template <int NW, bool MASK>
 HN_DEVICE void load_k(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int count) {
     const uint32_t t = threadIdx.x;
     const uint32_t last = (uint32_t)count - 1u;
@@ -192,6 +232,35 @@ HN_DEVICE void load_k(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int
         const uint32_t so = min(t & 63u, last) * (uint32_t)p.ss1;
         r.s = t < BKV ? tb.ks[so] : tb.vs[so];
     }
+    if constexpr (MASK) {
+        if ((t >> 6) == 2u) {
+            const uint32_t j = t & 63u;
+            r.mk = j <= last ? (tb.mk ? (uint32_t)tb.mk[j] : 1u) : 0u;
+        }
+    }
+}
+
+// The validity word of a cache tile, from the bytes wave 2 loaded with its
+// codes, into the stage (MASK only). Called with the tile's K write.
+template <int NW, bool MASK>
+HN_DEVICE void store_mask(const CacheRegs<NW>& r, uint8_t* st) {
+    if constexpr (MASK) {
+        if ((threadIdx.x >> 6) == 2) {
+            const uint64_t bits = __ballot(r.mk != 0u);
+            if ((threadIdx.x & 63) == 0) *reinterpret_cast<uint64_t*>(st + MASK_OFF) = bits;
+        }
+    }
+}
+
+// The validity word of the tile in stage st (ALL_KEYS without MASK). Every
+// lane reads the same 8 bytes; the word is made wave-uniform.
+template <bool MASK>
+HN_DEVICE uint64_t tile_mask(const uint8_t* st) {
+    if constexpr (!MASK) return ALL_KEYS;
+    const uint64_t w = *reinterpret_cast<const uint64_t*>(st + MASK_OFF);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)w);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
+    return ((uint64_t)hi << 32) | lo;
 }
 
 template <int NW>
@@ -244,9 +313,9 @@ HN_DEVICE void k_scales(const float* sb, float (&ks)[Shape<NW>::KU]) {
 }
 
 // Dequantized V^T write, part i (0..7): quad key j = i / 2, dims VD/2 (i % 2)
-// .. + VD/2 - 1 of the thread's VD; keys (0, 1) and (2, 3) pair into bf16
-// dwords (vd[2 d + pair], dim d), and parts 6 and 7 write the two halves of
-// the dims (8 bytes = 4 keys each).
+// .. + VD/2 - 1 of the thread's VD; keys (0, 1) and (2, 3) pair into dwords
+// of fp16-held bf16 values (vd[2 d + pair], dim d), and parts 6 and 7 write
+// the two halves of the dims (8 bytes = 4 keys each).
 template <int FMT, int NW>
 HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const float4& vs,
                             float (&vp)[Shape<NW>::VD], uint32_t (&vd)[2 * Shape<NW>::VD]) {
@@ -264,7 +333,7 @@ HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const fl
 #pragma unroll
     for (int dd = 0; dd < DP; ++dd) {
         const int d = DP * hf + dd;
-        if (j & 1) vd[2 * d + (j >> 1)] = pack_bf16(vp[d], x[dd]);
+        if (j & 1) vd[2 * d + (j >> 1)] = pack_f16_of_bf16(vp[d], x[dd]);
         else vp[d] = x[dd];
     }
     if (j == 3) {
@@ -285,8 +354,9 @@ HN_DEVICE float4 v_scales(const float* sb) {
 }
 
 // Whole-tile write (prologue), scales from the tile's scale buffer.
-template <int FMT, int NW>
+template <int FMT, int NW, bool MASK>
 HN_DEVICE void store_tile(const CacheRegs<NW>& r, uint8_t* st, const float* sb) {
+    store_mask<NW, MASK>(r, st);
     float ks[Shape<NW>::KU];
     k_scales<NW>(sb, ks);
     const float4 vs = v_scales(sb);
@@ -304,9 +374,18 @@ HN_DEVICE void store_tile(const CacheRegs<NW>& r, uint8_t* st, const float* sb) 
 // same thread-to-location mapping as the cache writes (so it cleanly
 // replaces what those wrote to the same stage). Not prefetched: it is at most
 // one chunk of the keys.
-template <int NW>
+template <int NW, bool MASK>
 HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
     const int t = threadIdx.x;
+    if constexpr (MASK) {
+        if ((t >> 6) == 2) {
+            const int j = t & 63;
+            uint32_t ok = 0u;
+            if (j < count) ok = p.uvalid ? (uint32_t)p.uvalid[b * p.uvs + first + j] : 1u;
+            const uint64_t bits = __ballot(ok != 0u);
+            if (j == 0) *reinterpret_cast<uint64_t*>(st + MASK_OFF) = bits;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < Shape<NW>::KU; ++i) {
         const int u = t + Shape<NW>::NT * i;
@@ -325,6 +404,7 @@ HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first,
     constexpr int VD = Shape<NW>::VD;
     const int qd = threadIdx.x & 15, dg = v_group<NW>();
     uint32_t w[4][VD / 2];  // dims VD dg .. + VD - 1 of quad key j (bf16 pairs)
+    // V^T holds fp16: the bf16 values converted (exactly, in fp16's range).
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = min(quad_key(qd, j), count - 1);
@@ -343,7 +423,8 @@ HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first,
         const uint32_t sh = (d & 1) * 16;
 #pragma unroll
         for (int pr = 0; pr < 2; ++pr)
-            o[pr] = ((w[2 * pr][d >> 1] >> sh) & 0xffffu) | (((w[2 * pr + 1][d >> 1] >> sh) & 0xffffu) << 16);
+            o[pr] = bf16x2_to_f16x2(((w[2 * pr][d >> 1] >> sh) & 0xffffu) |
+                                    (((w[2 * pr + 1][d >> 1] >> sh) & 0xffffu) << 16));
         *reinterpret_cast<uint2*>(st + K_BYTES + (VD * dg + d) * VTROW + 8 * qd) = make_uint2(o[0], o[1]);
     }
 }
@@ -352,16 +433,24 @@ HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+HN_DEVICE f32x16 mfma_f16(const f16x8& a, const f16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 HN_DEVICE bf16x8 ld_bf16x8(const uint8_t* p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
 }
 
-// Max of v over the lane pair (l, l ^ 32) with gfx950's half-wave swap.
-HN_DEVICE float pair_max(float v) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, v);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+HN_DEVICE f16x8 ld_f16x8(const uint8_t* p) {
+    return __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(p));
 }
+
+// Max of v over the lane pair (l, l ^ 32), through the LDS crossbar
+// (ds_bpermute). gfx950's v_permlane32_swap is not used: in this kernel's
+// instruction stream the compiler issues it two wait states after the VALU
+// write of its operand, and the swapped values were then stale (the running
+// max came out lane-local, which fp16 probabilities turn into overflow).
+HN_DEVICE float pair_max(float v) { return fmaxf(v, __shfl_xor(v, 32, 64)); }
 
 // ---------------------------------------------------------------------------
 // Half-tile steps. A "half" is one 32-key block kb of a 64-key tile; for it
@@ -386,12 +475,14 @@ HN_DEVICE float raw_max(const f32x16& s) {
     return pair_max(mx);
 }
 
-// Partial tiles: keys j >= lim of the tile are masked to -inf; returns the new max.
-HN_DEVICE float mask_raw(f32x16& s, int kb, int half, int lim) {
+// Partial tiles: keys j >= lim of the tile, and keys whose bit of the tile's
+// validity word mw is clear, are masked to -inf; returns the new max.
+HN_DEVICE float mask_raw(f32x16& s, int kb, int half, int lim, uint64_t mw) {
+    const uint32_t bits = (uint32_t)(mw >> (kb * 32 + 4 * half));
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        if (j >= lim) s[v] = -INFINITY;
+        if (j >= lim || !((bits >> (8 * (v >> 2) + (v & 3))) & 1u)) s[v] = -INFINITY;
     }
     return raw_max(s);
 }
@@ -439,9 +530,9 @@ HN_DEVICE void pin(A& a) {
 
 // Step A: S^T of the next block from the K rows at ka (this lane's row in the
 // stage) beside the probabilities of the current block (raw S^T in s):
-// p = 2^(s c - m), l += p, P^T = bf16(p) for the two 16-key slices (registers
+// p = 2^(s c - m), l += p, P^T = fp16(p) for the two 16-key slices (registers
 // 8t .. 8t+7 hold keys 16 t + 4 half + {0..3} and + 8 + {0..3} of the block).
-HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, bf16x8 (&pf)[2], const uint8_t* ka,
+HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, f16x8 (&pf)[2], const uint8_t* ka,
                         const bf16x8 (&qf)[8]) {
     const float nm = m == -INFINITY ? 0.0f : -m;  // m = -inf: every s is -inf (masked)
     bf16x8 kf[8];
@@ -460,13 +551,13 @@ HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, bf16x8 (&pf
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i + 1], c, nm));
         ls[0] += p0;
         ls[1] += p1;
-        x[i] = pack_bf16(p0, p1);
+        x[i] = pack_f16(p0, p1);
         pin(x[i], ls[0], ls[1]);
         __builtin_amdgcn_sched_barrier(0);
     }
     l += ls[0] + ls[1];
-    pf[0] = __builtin_bit_cast(bf16x8, make_uint4(x[0], x[1], x[2], x[3]));
-    pf[1] = __builtin_bit_cast(bf16x8, make_uint4(x[4], x[5], x[6], x[7]));
+    pf[0] = __builtin_bit_cast(f16x8, make_uint4(x[0], x[1], x[2], x[3]));
+    pf[1] = __builtin_bit_cast(f16x8, make_uint4(x[4], x[5], x[6], x[7]));
     return acc;
 }
 
@@ -475,12 +566,12 @@ HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, bf16x8 (&pf
 // per STORE (1: K, 2: V^T), half of the write of the prefetched tile to stage
 // nst with the scales of buffer sb. Returns the next block's raw max (pair-wide).
 template <int FMT, int NW, int STORE>
-HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (&o)[4], const f32x16& s,
+HN_DEVICE float step_b(const f16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (&o)[4], const f32x16& s,
                        const CacheRegs<NW>& r, uint8_t* nst, const float* sb) {
     // operand i (= 4 tt + db): dim block db, 16-key slice 2 kb + tt
-    bf16x8 vf[8];
-    vf[0] = ld_bf16x8(va + 64 * kb);
-    vf[1] = ld_bf16x8(va + 64 * kb + 32 * VTROW);
+    f16x8 vf[8];
+    vf[0] = ld_f16x8(va + 64 * kb);
+    vf[1] = ld_f16x8(va + 64 * kb + 32 * VTROW);
     float ks[Shape<NW>::KU] = {};
     float4 vs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (STORE == 1) k_scales<NW>(sb, ks);
@@ -494,9 +585,9 @@ HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 
         const int tt = i >> 2, db = i & 3;
         if (i + 2 < 8) {
             const int i2 = i + 2;
-            vf[i2] = ld_bf16x8(va + 64 * kb + 32 * (i2 >> 2) + (i2 & 3) * 32 * VTROW);
+            vf[i2] = ld_f16x8(va + 64 * kb + 32 * (i2 >> 2) + (i2 & 3) * 32 * VTROW);
         }
-        o[db] = mfma_bf16(vf[i], pf[tt], o[db]);
+        o[db] = mfma_f16(vf[i], pf[tt], o[db]);
         mx = fmaxf(mx, fmaxf(s[2 * i], s[2 * i + 1]));
         pin(mx);
         if (STORE == 1) store_k_part<FMT, NW>(r, nst, i, ks, kd);
@@ -506,7 +597,7 @@ HN_DEVICE float step_b(const bf16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 
     return pair_max(mx);
 }
 
-template <int FMT, int NW>
+template <int FMT, int NW, bool MASK>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     constexpr int BQ = Shape<NW>::BQ;
     constexpr int NS = stages<NW>();
@@ -637,25 +728,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
         if (t_end > t_begin) {
             f32x16 sa, sb;
             float mxa, mxb;
+            uint64_t mw;  // validity word of tile t
             Geom g = geom(t_begin);
             {
                 if (g.cache) {
                     const TileBase tb = tile_base(p, b, h, g.first);
-                    load_k<NW>(p, regs, tb, g.count);
+                    load_k<NW, MASK>(p, regs, tb, g.count);
                     load_v<NW>(p, regs, tb, g.count);
                     __builtin_amdgcn_s_waitcnt(0);
                     if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
                     __syncthreads();
-                    store_tile<FMT, NW>(regs, smem, sbuf);
+                    store_tile<FMT, NW, MASK>(regs, smem, sbuf);
                 } else {
-                    copy_tail_k<NW>(p, b, h, g.first, g.count, smem);
+                    copy_tail_k<NW, MASK>(p, b, h, g.first, g.count, smem);
                     copy_tail_v<NW>(p, b, h, g.first, g.count, smem);
                 }
                 if (t_begin + 1 < t_end) {
                     const Geom g1 = geom(t_begin + 1);
                     if (g1.cache) {
                         const TileBase tb = tile_base(p, b, h, g1.first);
-                        load_k<NW>(p, regs, tb, g1.count);
+                        load_k<NW, MASK>(p, regs, tb, g1.count);
                         load_v<NW>(p, regs, tb, g1.count);
                     }
                 }
@@ -664,8 +756,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 __builtin_amdgcn_s_waitcnt(0);
                 if (threadIdx.x < 2 * BKV) sbuf[SB_FLOATS + threadIdx.x] = regs.s;
                 __syncthreads();
+                mw = tile_mask<MASK>(smem);
                 sa = s_block(smem + ka_off, qf);
-                mxa = g.full ? raw_max(sa) : mask_raw(sa, 0, half, g.lim);
+                mxa = g.full && mw == ALL_KEYS ? raw_max(sa) : mask_raw(sa, 0, half, g.lim, mw);
             }
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
@@ -676,26 +769,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 const Geom gn = geom(has_next ? t + 1 : t);
                 const bool fetch2 = t + 2 < t_end;
                 const Geom g2 = geom(fetch2 ? t + 2 : t);
-                bf16x8 pf[2];
+                f16x8 pf[2];
 
                 // ---- half 0
                 rebase(mxa, c, m, l, o);
                 sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
-                // K of tile t + 1 from the prefetch registers (a tail tile or the
-                // end of the range is handled right after: the K rows of the stage
-                // are not read before the barrier).
+                // K (and validity word) of tile t + 1 from the prefetch registers
+                // (a tail tile or the end of the range is handled right after:
+                // the stage is not read before the barrier).
                 mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
-                if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
-                if (has_next && !gn.cache) copy_tail_k<NW>(p, b, h, gn.first, gn.count, nst);
-                if (fetch2 && g2.cache) load_k<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                store_mask<NW, MASK>(regs, nst);
+                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, g.lim, mw);
+                if (has_next && !gn.cache) copy_tail_k<NW, MASK>(p, b, h, gn.first, gn.count, nst);
+                if (fetch2 && g2.cache) load_k<NW, MASK>(p, regs, tile_base(p, b, h, g2.first), g2.count);
                 __syncthreads();
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
+                const uint64_t mwn = tile_mask<MASK>(nst);
                 rebase(mxb, c, m, l, o);
                 sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
-                if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
+                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
                 if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
                 if (fetch2 && g2.cache) {
                     if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
@@ -703,6 +798,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 }
                 __syncthreads();
                 g = gn;
+                mw = mwn;
             }
         }
     } else {
@@ -721,14 +817,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 const Geom gk = geom(t);
                 if (gk.cache) {
                     const TileBase tb = tile_base(p, b, h, gk.first);
-                    load_k<NW>(p, regs, tb, gk.count);
+                    load_k<NW, MASK>(p, regs, tb, gk.count);
                     load_v<NW>(p, regs, tb, gk.count);
                     __builtin_amdgcn_s_waitcnt(0);
                     if (threadIdx.x < 2 * BKV) sbuf[(k & 1) * SB_FLOATS + threadIdx.x] = regs.s;
                     __syncthreads();
-                    store_tile<FMT, NW>(regs, smem + k * STAGE, sbuf + (k & 1) * SB_FLOATS);
+                    store_tile<FMT, NW, MASK>(regs, smem + k * STAGE, sbuf + (k & 1) * SB_FLOATS);
                 } else {
-                    copy_tail_k<NW>(p, b, h, gk.first, gk.count, smem + k * STAGE);
+                    copy_tail_k<NW, MASK>(p, b, h, gk.first, gk.count, smem + k * STAGE);
                     copy_tail_v<NW>(p, b, h, gk.first, gk.count, smem + k * STAGE);
                 }
             }
@@ -736,7 +832,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 const Geom gk = geom(t_begin + NS - 1);
                 if (gk.cache) {
                     const TileBase tb = tile_base(p, b, h, gk.first);
-                    load_k<NW>(p, regs, tb, gk.count);
+                    load_k<NW, MASK>(p, regs, tb, gk.count);
                     load_v<NW>(p, regs, tb, gk.count);
                 }
             }
@@ -746,8 +842,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             if (threadIdx.x < 2 * BKV) sbuf[((NS - 1) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
             __syncthreads();
             Geom g = geom(t_begin);
+            uint64_t mw = tile_mask<MASK>(smem);  // validity word of tile t
             sa = s_block(smem + ka_off, qf);
-            mxa = g.full ? raw_max(sa) : mask_raw(sa, 0, half, g.lim);
+            mxa = g.full && mw == ALL_KEYS ? raw_max(sa) : mask_raw(sa, 0, half, g.lim, mw);
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
                 const uint8_t* st = smem + (u % NS) * STAGE;              // tile t
@@ -760,26 +857,27 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 const Geom gw = geom(write ? t + NS - 1 : t);
                 const bool fetch = t + NS < t_end;
                 const Geom gf = geom(fetch ? t + NS : t);
-                bf16x8 pf[2];
+                f16x8 pf[2];
+                const uint64_t mwn = tile_mask<MASK>(st1);  // tile t + 1 (stale on the last tile)
 
                 // ---- half 0
                 rebase(mxa, c, m, l, o);
                 sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
-                // K of tile t + NS - 1 from the prefetch registers (a tail tile or
-                // the end of the range is handled right after: the K rows of the
-                // stage are not read before the barrier).
+                // K (and validity word) of tile t + NS - 1 from the prefetch
+                // registers (a tail tile or the end of the range is handled
+                // right after: the stage is not read before the barrier).
                 mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
-                if (!g.full) mxb = mask_raw(sb, 1, half, g.lim);
-                if (write && !gw.cache) copy_tail_k<NW>(p, b, h, gw.first, gw.count, wst);
-                if (fetch && gf.cache) load_k<NW>(p, regs, tile_base(p, b, h, gf.first), gf.count);
-                if (NS == 2) __syncthreads();
+                store_mask<NW, MASK>(regs, wst);
+                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, g.lim, mw);
+                if (write && !gw.cache) copy_tail_k<NW, MASK>(p, b, h, gw.first, gw.count, wst);
+                if (fetch && gf.cache) load_k<NW, MASK>(p, regs, tile_base(p, b, h, gf.first), gf.count);
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
                 rebase(mxb, c, m, l, o);
                 sa = step_a(sb, c, m, l, pf, st1 + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
-                if (!gn.full) mxa = mask_raw(sa, 0, half, gn.lim);
+                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
                 if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
                 if (fetch && gf.cache) {
                     if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
@@ -787,6 +885,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 }
                 __syncthreads();
                 g = gn;
+                mw = mwn;
             }
         }
     }
@@ -945,6 +1044,15 @@ extern "C" int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H
     return plan_workspace(attn_plan(B, Lq, H, kv_len, cur_len), B, Lq, H);
 }
 
+// The kernel instantiation for the format, with or without key-validity masks.
+template <int NW, bool MASK>
+static void launch_kernel(const attn::Params& p, dim3 grid, hipStream_t stream) {
+    if (p.fmt == HN_KV_FP8)
+        attn::attn_fp8kv_kernel<HN_KV_FP8, NW, MASK><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
+    else
+        attn::attn_fp8kv_kernel<HN_KV_INT8, NW, MASK><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
+}
+
 // One launch of the NW-wave kernel over query rows [row0, row0 + rows) of p's
 // problem (p.Lq = all rows), with `sp` key-range splits merged through the
 // workspace by attn_combine_kernel.
@@ -966,10 +1074,8 @@ static int launch_rows(attn::Params p, int64_t B, int64_t row0, int64_t rows, in
     p.ws_o = sp > 1 ? (float*)workspace : nullptr;
     p.ws_ml = sp > 1 ? (float*)workspace + (int64_t)sp * B * p.H * rows * attn::D : nullptr;
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    if (p.fmt == HN_KV_FP8)
-        attn::attn_fp8kv_kernel<HN_KV_FP8, NW><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
-    else
-        attn::attn_fp8kv_kernel<HN_KV_INT8, NW><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
+    if (p.kvalid || p.uvalid) launch_kernel<NW, true>(p, grid, stream);
+    else launch_kernel<NW, false>(p, grid, stream);
     int rc = check_launch("hn_attn_fp8kv");
     if (rc != HN_OK || sp <= 1) return rc;
     const int64_t nrows = B * p.H * rows;
@@ -979,18 +1085,23 @@ static int launch_rows(attn::Params p, int64_t B, int64_t row0, int64_t rows, in
     return check_launch("hn_attn_fp8kv (combine)");
 }
 
-extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
-                             int64_t H, int64_t D, const void* kc, const void* vc,
-                             const int64_t* cs, const float* ks, const float* vs,
-                             const int64_t* ss, int64_t kv_len, const void* kcur,
-                             const void* vcur, const int64_t* curs, int64_t cur_len,
-                             int64_t q_pos0, int64_t chunk_len, float softmax_scale, void* out,
-                             const int64_t* os, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
+// Argument checks and parameter block shared by the attention entry points.
+// Returns HN_OK with *pp and *plan filled, or an error code (nothing enqueued).
+static int attn_setup(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq, int64_t H,
+                      int64_t D, const void* kc, const void* vc, const int64_t* cs, const float* ks,
+                      const float* vs, const int64_t* ss, int64_t cache_cap, int64_t kv_len,
+                      const uint8_t* cache_valid, int64_t cvs, const void* kcur, const void* vcur,
+                      const int64_t* curs, int64_t cur_len, const uint8_t* cur_valid, int64_t uvs,
+                      int64_t q_pos0, int64_t chunk_len, float softmax_scale, void* out,
+                      const int64_t* os, attn::Params* pp, AttnPlan* plan, bool* empty) {
     HN_REQUIRE(fmt == HN_KV_FP8 || fmt == HN_KV_INT8, HN_E_ARG, "hn_attn_fp8kv: unknown KV format");
     HN_REQUIRE(D == attn::D, HN_E_ARG, "hn_attn_fp8kv: head dim must be 128");
     HN_REQUIRE(B >= 0 && Lq >= 0 && H > 0 && kv_len >= 0 && cur_len >= 0 && q_pos0 >= 0, HN_E_ARG,
                "hn_attn_fp8kv: invalid shape");
+    HN_REQUIRE(kv_len <= cache_cap, HN_E_ARG, "hn_attn_fp8kv: kv_len exceeds the cache capacity");
+    HN_REQUIRE(softmax_scale > 0.0f && softmax_scale <= 3.4028234e38f, HN_E_ARG,
+               "hn_attn_fp8kv: softmax_scale must be finite and positive");
+    HN_REQUIRE(cvs >= 0 && uvs >= 0, HN_E_ARG, "hn_attn_fp8kv: negative validity stride");
     HN_REQUIRE(qs && os && (kv_len == 0 || (cs && ss)) && (cur_len == 0 || curs), HN_E_ARG,
                "hn_attn_fp8kv: null stride array");
     HN_REQUIRE(qs[3] == 1 && os[3] == 1, HN_E_ARG, "hn_attn_fp8kv: head dim must be contiguous");
@@ -1002,6 +1113,8 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
         HN_REQUIRE(kc && vc && ks && vs, HN_E_ARG, "hn_attn_fp8kv: null cache pointer");
         HN_REQUIRE(cs[3] == 1 && cs[0] % 16 == 0 && cs[1] % 16 == 0 && cs[2] % 16 == 0, HN_E_ARG,
                    "hn_attn_fp8kv: cache strides must be multiples of 16 bytes");
+        HN_REQUIRE(cs[0] >= 0 && cs[1] > 0 && cs[2] >= 0 && ss[0] >= 0 && ss[1] > 0 && ss[2] >= 0,
+                   HN_E_ARG, "hn_attn_fp8kv: invalid cache strides");
         HN_REQUIRE(aligned(kc, 16) && aligned(vc, 16), HN_E_ARG, "hn_attn_fp8kv: cache misaligned");
     }
     if (cur_len > 0) {
@@ -1010,14 +1123,20 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
                    HN_E_ARG, "hn_attn_fp8kv: tail strides must be multiples of 8");
         HN_REQUIRE(aligned(kcur, 16) && aligned(vcur, 16), HN_E_ARG, "hn_attn_fp8kv: tail misaligned");
     }
-    if (B == 0 || Lq == 0) return HN_OK;
+    *empty = B == 0 || Lq == 0;
+    if (*empty) return HN_OK;
     HN_REQUIRE(out && q, HN_E_ARG, "hn_attn_fp8kv: null q/out");
-    attn::Params p;
+    const int rc = require_gfx950("hn_attn_fp8kv");
+    if (rc != HN_OK) return rc;
+    attn::Params& p = *pp;
     p.q = (const uint16_t*)q;
     p.kc = (const uint8_t*)kc; p.vc = (const uint8_t*)vc;
     p.ks = ks; p.vs = vs;
     p.kcur = (const uint16_t*)kcur; p.vcur = (const uint16_t*)vcur;
     p.out = (uint16_t*)out;
+    p.kvalid = kv_len > 0 ? cache_valid : nullptr;
+    p.uvalid = cur_len > 0 ? cur_valid : nullptr;
+    p.kvs = cvs; p.uvs = uvs;
     p.qs0 = qs[0]; p.qs1 = qs[1]; p.qs2 = qs[2];
     if (kv_len > 0) {
         p.cs0 = cs[0]; p.cs1 = cs[1]; p.cs2 = cs[2];
@@ -1035,14 +1154,38 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
     p.q_pos0 = q_pos0; p.chunk = chunk_len;
     p.scale_log2 = softmax_scale * 1.4426950408889634f;
     p.fmt = fmt;
-    const AttnPlan plan = attn_plan(B, Lq, H, kv_len, cur_len);
-    const int64_t need = plan_workspace(plan, B, Lq, H);
-    HN_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))), HN_E_ARG,
-               "hn_attn_fp8kv: workspace smaller than hn_attn_fp8kv_workspace_size() or misaligned");
-    const hipStream_t st = (hipStream_t)stream;
+    *plan = attn_plan(B, Lq, H, kv_len, cur_len);
+    return HN_OK;
+}
+
+static int attn_run(const attn::Params& p, const AttnPlan& plan, int64_t B, int64_t Lq, void* workspace,
+                    hipStream_t st) {
     if (plan.rows8 > 0) {
         const int rc = launch_rows<8>(p, B, 0, plan.rows8, 1, nullptr, st);
         if (rc != HN_OK || plan.rows8 == Lq) return rc;
     }
     return launch_rows<4>(p, B, plan.rows8, Lq - plan.rows8, plan.splits, workspace, st);
+}
+
+extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
+                             int64_t H, int64_t D, const void* kc, const void* vc,
+                             const int64_t* cs, const float* ks, const float* vs,
+                             const int64_t* ss, int64_t cache_cap, int64_t kv_len,
+                             const uint8_t* cache_valid, int64_t cache_valid_stride,
+                             const void* kcur, const void* vcur, const int64_t* curs,
+                             int64_t cur_len, const uint8_t* cur_valid, int64_t cur_valid_stride,
+                             int64_t q_pos0, int64_t chunk_len, float softmax_scale, void* out,
+                             const int64_t* os, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+    attn::Params p;
+    AttnPlan plan;
+    bool empty = false;
+    int rc = attn_setup(fmt, q, qs, B, Lq, H, D, kc, vc, cs, ks, vs, ss, cache_cap, kv_len, cache_valid,
+                        cache_valid_stride, kcur, vcur, curs, cur_len, cur_valid, cur_valid_stride, q_pos0,
+                        chunk_len, softmax_scale, out, os, &p, &plan, &empty);
+    if (rc != HN_OK || empty) return rc;
+    const int64_t need = plan_workspace(plan, B, Lq, H);
+    HN_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))), HN_E_ARG,
+               "hn_attn_fp8kv: workspace smaller than hn_attn_fp8kv_workspace_size() or misaligned");
+    return attn_run(p, plan, B, Lq, workspace, (hipStream_t)stream);
 }

@@ -1216,6 +1216,7 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
                HN_E_ARG, "FP8 GEMM: misaligned pointer");
     if (M == 0) return HN_OK;
     HN_REQUIRE(a && b && sa && sb && out, HN_E_ARG, "FP8 GEMM: null pointer");
+    if (const int rc = require_gfx950(who); rc != HN_OK) return rc;
     gemm::Params p;
     p.a = (const uint8_t*)a; p.b = (const uint8_t*)b;
     p.sa = sa; p.sb = sb;

@@ -32,6 +32,10 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 // Compute units of the current device (256 if the query fails).
 int device_cus();
 
+// HN_OK if the current device is a gfx950; otherwise records "<who>: ..." and
+// returns HN_E_DEVICE. The architecture is looked up once per device.
+int require_gfx950(const char* who);
+
 // Grid for the streaming kernels' grid-stride loops: `per_cu` workgroups per
 // CU, fewer when there is less work. A moderate resident grid walking the
 // data in order sustains more HBM bandwidth on a mixed read/write stream than

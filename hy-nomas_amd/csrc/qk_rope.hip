@@ -40,6 +40,10 @@ struct Args {
     float* sk;
     float* sv;
     int64_t qs0, qs1, qs2, ss0, ss1, ss2, start;
+    // Device-side validation of the cache write (null: unchecked): set to 1 by
+    // qk_check_kernel when a value to be written is NaN/Inf; the cache write
+    // (not the in-place q/k update) is then skipped.
+    int32_t* status;
 };
 
 HN_DEVICE void unpack8(const uint4& v, float (&f)[8]) {
@@ -96,6 +100,42 @@ HN_DEVICE void quantize_row(const float (&f)[8], uint8_t* code_row, float* scale
     if (lane16 == 0) *scale = s;
 }
 
+// The values one row would write into the cache: the rotated k (bf16, as
+// stored in place) and v, checked for NaN/Inf with the same arithmetic as
+// qk_norm_rope_kernel, so the check tests exactly what would be written. Sets
+// *a.status = 1 if any is not finite (the flag is cleared beforehand).
+__global__ __launch_bounds__(256) void qk_check_kernel(Args a) {
+    const int lane16 = threadIdx.x & 15;
+    uint32_t bad = 0u;
+    for (int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4); row < a.rows;
+         row += (int64_t)gridDim.x * 16) {  // grid-stride over whole 16-lane groups
+        const int64_t h = row % a.H;
+        const int64_t t = (row / a.H) % a.L;
+        const int64_t b = row / (a.H * a.L);
+        const int64_t off = b * a.xs0 + t * a.xs1 + h * a.xs2 + lane16 * 8;
+        float kx[8], w[8], c[8], s[8];
+        unpack8(*reinterpret_cast<const uint4*>(a.k + off), kx);
+        const float4* cp = reinterpret_cast<const float4*>(a.cos + t * a.cs + lane16 * 8);
+        const float4* sp = reinterpret_cast<const float4*>(a.sin + t * a.cs + lane16 * 8);
+        const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+        c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+        s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w; s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+        unpack8(*reinterpret_cast<const uint4*>(a.kw + lane16 * 8), w);
+        norm_rope(kx, w, c, s, a.eps);
+        const uint4 ko = pack8(kx);
+        const uint4 vo = *reinterpret_cast<const uint4*>(a.v + off);
+        const uint32_t wd[8] = {ko.x, ko.y, ko.z, ko.w, vo.x, vo.y, vo.z, vo.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)  // bf16 exponent all ones: Inf or NaN
+            bad |= (uint32_t)((wd[j] & 0x7f80u) == 0x7f80u) | (uint32_t)(((wd[j] >> 16) & 0x7f80u) == 0x7f80u);
+    }
+    if (__any(bad != 0u) && (threadIdx.x & 63) == 0) *a.status = 1;
+}
+
+__global__ void qk_status_clear_kernel(int32_t* status) {
+    if (threadIdx.x == 0) *status = 0;
+}
+
 template <int FMT, bool CACHE>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(Args a) {
     const int lane16 = threadIdx.x & 15;
@@ -122,7 +162,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(Args a) {
     *reinterpret_cast<uint4*>(a.q + off) = qo;
     *reinterpret_cast<uint4*>(a.k + off) = ko;
 
-    if (CACHE) {
+    if (CACHE && (a.status == nullptr || *a.status == 0)) {
         float kr[8], vx[8];
         unpack8(ko, kr);  // the rounded bf16 values that were stored
         unpack8(*reinterpret_cast<const uint4*>(a.v + off), vx);
@@ -143,8 +183,8 @@ extern "C" int hn_qk_norm_rope_kv(int fmt, void* q, void* k, const void* v, cons
                                   int64_t B, int64_t L, int64_t H, int64_t D, const void* q_weight,
                                   const void* k_weight, const float* cos_t, const float* sin_t,
                                   int64_t cs, float eps, void* kc, void* vc, const int64_t* qs,
-                                  float* ks, float* vs, const int64_t* ss, int64_t start,
-                                  void* stream) {
+                                  float* ks, float* vs, const int64_t* ss, int64_t cap,
+                                  int64_t start, int32_t* status, void* stream) {
     HN_REQUIRE(fmt == HN_KV_FP8 || fmt == HN_KV_INT8, HN_E_ARG, "hn_qk_norm_rope_kv: unknown KV format");
     HN_REQUIRE(D == 128, HN_E_ARG, "hn_qk_norm_rope_kv: head dim must be 128");
     HN_REQUIRE(B >= 0 && L >= 0 && H > 0 && start >= 0, HN_E_ARG, "hn_qk_norm_rope_kv: invalid shape");
@@ -161,11 +201,17 @@ extern "C" int hn_qk_norm_rope_kv(int fmt, void* q, void* k, const void* v, cons
                    "hn_qk_norm_rope_kv: cache strides must be multiples of 8 bytes");
         HN_REQUIRE(aligned(kc, 8) && aligned(vc, 8) && aligned(ks, 4) && aligned(vs, 4), HN_E_ARG,
                    "hn_qk_norm_rope_kv: misaligned cache pointer");
+        HN_REQUIRE(cap >= 0 && start <= cap && L <= cap - start, HN_E_ARG,
+                   "hn_qk_norm_rope_kv: KV write past the cache capacity (start + L > cap)");
+        HN_REQUIRE(aligned(status, 4), HN_E_ARG, "hn_qk_norm_rope_kv: misaligned status pointer");
+    } else {
+        HN_REQUIRE(status == nullptr, HN_E_ARG, "hn_qk_norm_rope_kv: status without a cache write");
     }
     const int64_t rows = B * L * H;
     if (rows == 0) return HN_OK;
     HN_REQUIRE(q && k && v && q_weight && k_weight && cos_t && sin_t, HN_E_ARG,
                "hn_qk_norm_rope_kv: null pointer");
+    if (const int rc = require_gfx950("hn_qk_norm_rope_kv"); rc != HN_OK) return rc;
     qkr::Args a;
     a.q = (uint16_t*)q; a.k = (uint16_t*)k; a.v = (const uint16_t*)v;
     a.xs0 = xs[0]; a.xs1 = xs[1]; a.xs2 = xs[2];
@@ -176,10 +222,15 @@ extern "C" int hn_qk_norm_rope_kv(int fmt, void* q, void* k, const void* v, cons
     a.qs0 = cache ? qs[0] : 0; a.qs1 = cache ? qs[1] : 0; a.qs2 = cache ? qs[2] : 0;
     a.ss0 = cache ? ss[0] : 0; a.ss1 = cache ? ss[1] : 0; a.ss2 = cache ? ss[2] : 0;
     a.start = start;
+    a.status = status;
     const int64_t blocks = (rows + 15) / 16;
     HN_REQUIRE(blocks <= 0x7fffffffLL, HN_E_ARG, "hn_qk_norm_rope_kv: too many rows");
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)blocks);
+    if (status) {
+        qkr::qk_status_clear_kernel<<<1, 64, 0, st>>>(status);
+        qkr::qk_check_kernel<<<(unsigned)stream_grid(blocks, 8), 256, 0, st>>>(a);
+    }
     if (!cache)
         qkr::qk_norm_rope_kernel<HN_KV_FP8, false><<<grid, 256, 0, st>>>(a);
     else if (fmt == HN_KV_FP8)

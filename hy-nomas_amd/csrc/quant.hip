@@ -310,7 +310,57 @@ struct KvArgs {
     // ceil(H / 8)); otherwise 64 consecutive (token, head) rows of one batch
     // (ttiles = ceil(L * H / 64) per batch, L * H < 2^31).
     int64_t ttiles, htiles, units;
+    // Device-side validation (null: unchecked): set by kv_check_kernel when a
+    // value is NaN/Inf; the write then stores nothing.
+    const int32_t* status;
 };
+
+// Validate-before-write on the device (the reference's check,
+// int8_kv_cache.py:140-141,176, without its host synchronisation):
+// status_clear_kernel zeroes the flag, kv_check_kernel sets it to 1 when any
+// value of the one or two sources (blockIdx.y) is NaN or Inf, and the write
+// kernel that follows on the stream reads it and writes nothing when it is
+// set. The flag is cleared by a kernel rather than a memset so that the
+// sequence can be recorded in a graph.
+__global__ void status_clear_kernel(int32_t* status) {
+    if (threadIdx.x == 0) *status = 0;
+}
+
+struct KvCheckArgs {
+    const uint16_t* x[2];
+    int64_t xs0, xs1, xs2;
+    int64_t L, H, rows;
+    int32_t* status;
+};
+
+// One (batch, token, head) row of 128 bf16 per 16-lane group, 8 per lane, in
+// a grid-stride loop; rows are walked token-fastest when the source's token
+// stride is the smaller one, so that consecutive groups read adjacent rows.
+template <bool TOKEN_FAST>
+__global__ __launch_bounds__(256) void kv_check_kernel(KvCheckArgs a) {
+    const uint16_t* x = a.x[blockIdx.y];
+    const int lane16 = threadIdx.x & 15;
+    uint32_t bad = 0u;
+    for (int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4); row < a.rows;
+         row += (int64_t)gridDim.x * 16) {
+        int64_t b, t, h;
+        if (TOKEN_FAST) {
+            t = row % a.L;
+            h = (row / a.L) % a.H;
+            b = row / (a.L * a.H);
+        } else {
+            h = row % a.H;
+            t = (row / a.H) % a.L;
+            b = row / (a.L * a.H);
+        }
+        const uint4 v = *reinterpret_cast<const uint4*>(x + b * a.xs0 + t * a.xs1 + h * a.xs2 + lane16 * 8);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)  // bf16 exponent all ones: Inf or NaN
+            bad |= (uint32_t)((w[j] & 0x7f80u) == 0x7f80u) | (uint32_t)(((w[j] >> 16) & 0x7f80u) == 0x7f80u);
+    }
+    if (__any(bad != 0u) && (threadIdx.x & 63) == 0) *a.status = 1;
+}
 
 constexpr int KV_ROWS_PER_GROUP = 4;  // rows each 16-lane group carries (loads issued together)
 constexpr int KV_UNIT = 16 * KV_ROWS_PER_GROUP;
@@ -324,6 +374,7 @@ template <int FMT, bool TOKEN_FAST>
 __global__ __launch_bounds__(256) void kv_quantize_kernel(KvArgs a) {
     const int sel = blockIdx.y;
     const int lane16 = threadIdx.x & 15;
+    if (a.status != nullptr && *a.status != 0) return;  // rejected: write nothing
     for (int64_t unit = blockIdx.x; unit < a.units; unit += gridDim.x) {  // grid-stride
     // Group g (16 lanes) takes 4 rows, k = 0..3. TOKEN_FAST: token 8 tt + g % 8
     // of heads 8 ht + 4 (g / 8) + k -- for each k the loads are two runs of 8
@@ -445,6 +496,7 @@ extern "C" int hn_quantize_rows_fp8(const void* x, int64_t rows, int64_t cols,
                "hn_quantize_rows_fp8: x must be 16-byte and q 8-byte aligned");
     if (rows == 0) return HN_OK;
     HN_REQUIRE(x && q && scale, HN_E_ARG, "hn_quantize_rows_fp8: null pointer");
+    if (const int rc = require_gfx950("hn_quantize_rows_fp8"); rc != HN_OK) return rc;
     HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_quantize_rows_fp8: too many rows");
     const int per_lane = (int)((cols / 8 + 63) / 64);  // 16-byte chunks per lane, <= 32
     const dim3 grid((unsigned)stream_grid((rows + 3) / 4, 8));
@@ -493,6 +545,7 @@ extern "C" int hn_ln_mod_quantize_fp8(const void* x, int64_t rows, int64_t cols,
                HN_E_ARG, "hn_ln_mod_quantize_fp8: x, shift, scale_mod must be 16-byte and q 8-byte aligned");
     if (rows == 0) return HN_OK;
     HN_REQUIRE(x && shift && scale_mod && q && scale, HN_E_ARG, "hn_ln_mod_quantize_fp8: null pointer");
+    if (const int rc = require_gfx950("hn_ln_mod_quantize_fp8"); rc != HN_OK) return rc;
     HN_REQUIRE(rows <= 0x7fffffffLL, HN_E_ARG, "hn_ln_mod_quantize_fp8: too many rows");
     const int per_lane = (int)((cols / 8 + 63) / 64);  // 16-byte chunks per lane, <= 16
     const dim3 grid((unsigned)stream_grid((rows + 3) / 4, 8));
@@ -527,6 +580,7 @@ extern "C" int hn_quantize_blockwise_fp8(const void* x, int64_t rows, int64_t co
                "hn_quantize_blockwise_fp8: misaligned pointer");
     if (rows == 0) return HN_OK;
     HN_REQUIRE(x && q && scale, HN_E_ARG, "hn_quantize_blockwise_fp8: null pointer");
+    if (const int rc = require_gfx950("hn_quantize_blockwise_fp8"); rc != HN_OK) return rc;
     const dim3 grid((unsigned)((rows + 127) / 128), (unsigned)(cols / 128));
     quantize_blockwise_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, rows, cols, (uint8_t*)q, scale);
@@ -536,10 +590,13 @@ extern "C" int hn_quantize_blockwise_fp8(const void* x, int64_t rows, int64_t co
 static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_t* xs,
                             int64_t B, int64_t L, int64_t H, int64_t D, void* const q[2],
                             const int64_t* qs, float* const s[2], const int64_t* ss,
-                            int64_t start, void* stream, const char* who) {
+                            int64_t cap, int64_t start, int32_t* status, void* stream,
+                            const char* who) {
     if (fmt != HN_KV_FP8 && fmt != HN_KV_INT8) return fail(HN_E_ARG, "unknown KV format");
     HN_REQUIRE(D == 128, HN_E_ARG, "KV quantization requires head dim 128");
     HN_REQUIRE(B >= 0 && L >= 0 && H > 0 && start >= 0, HN_E_ARG, "invalid KV shape");
+    HN_REQUIRE(cap >= 0 && start <= cap && L <= cap - start, HN_E_ARG,
+               "KV write past the cache capacity (start + L > cap)");
     HN_REQUIRE(xs && qs && ss, HN_E_ARG, "null stride array");
     HN_REQUIRE(xs[3] == 1 && qs[3] == 1, HN_E_ARG, "KV head dim must be contiguous");
     HN_REQUIRE(xs[0] % 8 == 0 && xs[1] % 8 == 0 && xs[2] % 8 == 0, HN_E_ARG,
@@ -549,9 +606,11 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
     for (int i = 0; i < n; ++i)
         HN_REQUIRE(aligned(x[i], 16) && aligned(q[i], 8) && aligned(s[i], 4), HN_E_ARG,
                    "misaligned KV pointer");
+    HN_REQUIRE(aligned(status, 4), HN_E_ARG, "misaligned KV status pointer");
     const int64_t rows = B * L * H;
     if (rows == 0) return HN_OK;
     for (int i = 0; i < n; ++i) HN_REQUIRE(x[i] && q[i] && s[i], HN_E_ARG, "null KV pointer");
+    if (const int rc = require_gfx950(who); rc != HN_OK) return rc;
     KvArgs a;
     for (int i = 0; i < 2; ++i) {
         a.x[i] = (const uint16_t*)x[i < n ? i : 0];
@@ -569,6 +628,18 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
     a.ttiles = token_fast ? (L + 7) / 8 : (L * H + KV_UNIT - 1) / KV_UNIT;
     a.units = B * a.htiles * a.ttiles;
     const dim3 grid((unsigned)stream_grid(a.units, 16 / n), (unsigned)n);
+    a.status = status;
+    if (status) {
+        const hipStream_t st = (hipStream_t)stream;
+        status_clear_kernel<<<1, 64, 0, st>>>(status);
+        KvCheckArgs c;
+        for (int i = 0; i < 2; ++i) c.x[i] = a.x[i];
+        c.xs0 = xs[0]; c.xs1 = xs[1]; c.xs2 = xs[2];
+        c.L = L; c.H = H; c.rows = rows; c.status = status;
+        const dim3 cgrid((unsigned)stream_grid((rows + 15) / 16, 8 / n), (unsigned)n);
+        if (token_fast) kv_check_kernel<true><<<cgrid, 256, 0, st>>>(c);
+        else kv_check_kernel<false><<<cgrid, 256, 0, st>>>(c);
+    }
     if (fmt == HN_KV_FP8) {
         if (token_fast) kv_quantize_kernel<HN_KV_FP8, true><<<grid, 256, 0, (hipStream_t)stream>>>(a);
         else kv_quantize_kernel<HN_KV_FP8, false><<<grid, 256, 0, (hipStream_t)stream>>>(a);
@@ -581,22 +652,24 @@ static int kv_quantize_impl(int fmt, const void* const x[2], int n, const int64_
 
 extern "C" int hn_kv_quantize(int fmt, const void* x, const int64_t* xs, int64_t B, int64_t L,
                               int64_t H, int64_t D, void* q, const int64_t* qs, float* scale,
-                              const int64_t* ss, int64_t start, void* stream) {
+                              const int64_t* ss, int64_t cap, int64_t start, int32_t* status,
+                              void* stream) {
     const void* xx[2] = {x, x};
     void* qq[2] = {q, q};
     float* sss[2] = {scale, scale};
-    return kv_quantize_impl(fmt, xx, 1, xs, B, L, H, D, qq, qs, sss, ss, start, stream,
+    return kv_quantize_impl(fmt, xx, 1, xs, B, L, H, D, qq, qs, sss, ss, cap, start, status, stream,
                             "hn_kv_quantize");
 }
 
 extern "C" int hn_kv_quantize_pair(int fmt, const void* k, const void* v, const int64_t* xs,
                                    int64_t B, int64_t L, int64_t H, int64_t D, void* qk,
                                    void* qv, const int64_t* qs, float* sk, float* sv,
-                                   const int64_t* ss, int64_t start, void* stream) {
+                                   const int64_t* ss, int64_t cap, int64_t start, int32_t* status,
+                                   void* stream) {
     const void* xx[2] = {k, v};
     void* qq[2] = {qk, qv};
     float* sss[2] = {sk, sv};
-    return kv_quantize_impl(fmt, xx, 2, xs, B, L, H, D, qq, qs, sss, ss, start, stream,
+    return kv_quantize_impl(fmt, xx, 2, xs, B, L, H, D, qq, qs, sss, ss, cap, start, status, stream,
                             "hn_kv_quantize_pair");
 }
 
@@ -616,6 +689,7 @@ extern "C" int hn_kv_dequantize(int fmt, const void* q, const int64_t* qs, const
     const int64_t rows = B * valid_len * H;
     if (rows == 0) return HN_OK;
     HN_REQUIRE(q && scale && y, HN_E_ARG, "null KV decode pointer");
+    if (const int rc = require_gfx950("hn_kv_dequantize"); rc != HN_OK) return rc;
     KvDecArgs a;
     a.q = (const uint8_t*)q; a.s = scale; a.y = (uint16_t*)y;
     a.qs0 = qs[0]; a.qs1 = qs[1]; a.qs2 = qs[2];

@@ -26,7 +26,7 @@ import torch.nn.functional as F
 from . import ops
 from .cache_attention import chunk_attention
 from .dit_fp8_linear import FP8StoredLinear, fp8_linear, fp8_linear_codes
-from .fp8_kv_cache import make_fp8_kv_block, quantize_kv_pair_into
+from .fp8_kv_cache import make_fp8_kv_block
 from .metrics import stage
 
 
@@ -58,9 +58,10 @@ class FP8DiTBlock(nn.Module):
         super().__init__()
         self.hidden, self.heads, self.head_dim = hidden, heads, hidden // heads
         self.qk_eps = qk_eps
-        # True: the cache write validates K and V (finite) before writing either,
-        # as quantize_kv_pair_into does (one host sync per write pass). False:
-        # the write is fused into the QK norm/RoPE kernel, unvalidated.
+        # The cache write is fused into the QK norm/RoPE kernel. True: the
+        # values it would write are validated on the device first and nothing
+        # is written if one is NaN/Inf (the reference's validate-before-write,
+        # int8_kv_cache.py:161-179), flagged in a status word. False: unchecked.
         self.validate_kv_writes = validate_kv_writes
         # True: LayerNorm + modulate + the per-token FP8 quantization of the QKV
         # and fc1 inputs run as one kernel (ops.ln_modulate_quantize_fp8).
@@ -85,13 +86,16 @@ class FP8DiTBlock(nn.Module):
     def _fused(self, linear) -> bool:
         return self.fuse_ln_quant and isinstance(linear, FP8StoredLinear)
 
-    def pre_attention(self, img, vec, cos, sin, kv_cache=None, cache_start: int = 0):
+    def pre_attention(self, img, vec, cos, sin, kv_cache=None, cache_start: int = 0,
+                      kv_status=None):
         """Image-stream half of nomas_compile_prepost.pre_attention (:29-72):
         adaLN parts, LayerNorm + modulate, fused FP8 QKV, then per-head RMSNorm
         and RoPE in one kernel, in place on the QKV output. Returns q, k, v
         [B, L, H, D] bf16 (views of that output) and the six modulation parts.
         With ``kv_cache`` given, the rotated K and V are also written into it at
-        ``cache_start`` by the same kernel (unvalidated)."""
+        ``cache_start`` by the same kernel; with ``kv_status`` (int32 on the
+        device) that write is validated first and skipped, status[0] = 1, if
+        any value is NaN/Inf."""
         B, L, C = img.shape
         H, D = self.heads, self.head_dim
         with stage("modulation"):
@@ -114,7 +118,7 @@ class FP8DiTBlock(nn.Module):
             else:
                 ops.qk_norm_rope_kv_(q, k, v, self.q_norm, self.k_norm, cos, sin, self.qk_eps,
                                      kv_cache["k"], kv_cache["v"], kv_cache["k_scale"],
-                                     kv_cache["v_scale"], cache_start)
+                                     kv_cache["v_scale"], cache_start, kv_status)
         return q, k, v, parts
 
     def post_attention(self, img, attn, parts):
@@ -135,13 +139,20 @@ class FP8DiTBlock(nn.Module):
         return img
 
     def forward(self, img, vec, cos, sin, kv_cache, cache_valid_len: int,
-                update_cache: bool = False):
-        fused = update_cache and not self.validate_kv_writes
-        q, k, v, parts = self.pre_attention(img, vec, cos, sin, kv_cache if fused else None,
-                                            cache_valid_len)
+                update_cache: bool = False, kv_status=None):
+        """One block at inference. With ``update_cache`` this chunk's rotated K
+        and V go into ``kv_cache`` at ``cache_valid_len``. When writes are
+        validated and no ``kv_status`` is passed, a non-finite value raises
+        ValueError here (one host read of the device flag); with one, the flag
+        is left for the caller to read."""
+        status = None
         if update_cache and self.validate_kv_writes:
-            with stage("kv_write_fp8"):
-                quantize_kv_pair_into(kv_cache, k, v, cache_valid_len)
+            status = kv_status if kv_status is not None else torch.empty(
+                1, dtype=torch.int32, device=img.device)
+        q, k, v, parts = self.pre_attention(img, vec, cos, sin, kv_cache if update_cache else None,
+                                            cache_valid_len, status)
+        if status is not None and kv_status is None and int(status[0].item()):
+            raise ValueError("Cannot quantize non-finite KV values")
         with stage("cache_attention"):
             attn = chunk_attention(q, kv_cache, cache_valid_len, k_cur=k, v_cur=v)
         return self.post_attention(img, attn, parts)
@@ -165,6 +176,8 @@ class FP8ARModel(nn.Module):
         self.device = device
         self.caches = [make_fp8_kv_block(1, self.capacity, heads, self.head_dim, device=device)
                        for _ in range(depth)]
+        # one device status word per layer for the validated cache writes
+        self.kv_status = torch.zeros(depth, dtype=torch.int32, device=device)
         self.cache_valid_len = 0
         self.frames_done = 0
 
@@ -172,18 +185,33 @@ class FP8ARModel(nn.Module):
     def forward_chunk(self, img, vec, update_cache: bool):
         t, h, w = self.latent_shape
         cos, sin = rope_tables(t, h, w, t_offset=self.frames_done, device=img.device)
-        for block, cache in zip(self.blocks, self.caches):
-            img = block(img, vec, cos, sin, cache, self.cache_valid_len, update_cache)
+        for i, (block, cache) in enumerate(zip(self.blocks, self.caches)):
+            img = block(img, vec, cos, sin, cache, self.cache_valid_len, update_cache,
+                        kv_status=self.kv_status[i:i + 1] if update_cache else None)
         return img
 
     @torch.no_grad()
     def generate_chunk(self, noise, vecs_denoise, vec_write, sigmas):
-        """Euler flow updates over the denoising passes, then the cache write."""
+        """Euler flow updates over the denoising passes, then the cache write
+        at t = 0 and the advance of the valid length (causal_ar.py:2348-2432,
+        2624-2645,2852). A chunk that would not fit the cache is refused
+        before any pass runs. In the write pass a layer whose K/V holds a
+        NaN/Inf writes nothing; the valid length then stays where it was (rows
+        that other layers wrote past it are never attended) and ValueError
+        names the layers."""
+        if self.cache_valid_len + self.tokens_per_chunk > self.capacity:
+            raise ValueError(f"KV cache full: {self.cache_valid_len} + {self.tokens_per_chunk} tokens "
+                             f"exceed the capacity {self.capacity}")
+        if len(sigmas) != len(vecs_denoise) + 1:
+            raise ValueError("sigmas must hold one more value than the denoising passes")
         x = noise
         for i, vec in enumerate(vecs_denoise):
             v_pred = self.forward_chunk(x, vec, update_cache=False)
             x = x + (sigmas[i + 1] - sigmas[i]) * v_pred
         self.forward_chunk(x, vec_write, update_cache=True)
+        bad = torch.nonzero(self.kv_status).flatten().tolist()
+        if bad:
+            raise ValueError(f"Cannot quantize non-finite KV values (layers {bad})")
         self.cache_valid_len += self.tokens_per_chunk
         self.frames_done += self.latent_shape[0]
         return x

@@ -1,14 +1,17 @@
 /*
  * hynomas_fp8.h -- C ABI of the MI355X (gfx950) FP8 quantized inference path.
  *
- * One shared library, libhynomas_fp8.so, built from hy-nomas_amd/csrc/*.hip.
+ * One shared library, libhynomas_fp8.so, built from the HIP sources in
+ * hy-nomas_amd/csrc/.
  * Every pointer argument is a device pointer unless stated otherwise; sizes
  * and strides are in elements; `stream` is a hipStream_t (NULL = default
  * stream). Calls are asynchronous with respect to the host: they enqueue work
  * on `stream` and return. Each function returns HN_OK (0) or a negative HN_E*
  * code; hn_last_error() then describes the failure (thread-local). Argument
  * errors are detected on the host before anything is enqueued, so a failed
- * call has written nothing.
+ * call has written nothing. A call with work to do on a device that is not a
+ * gfx950 returns HN_E_DEVICE (the architecture check of the reference's
+ * extension, cutlass_fp8.cu:21-34).
  *
  * Byte formats: bf16 is IEEE bfloat16; e4m3 is OCP FP8 E4M3 ("fn": no
  * infinities, 0x7F/0xFF NaN, max 448), the format of torch.float8_e4m3fn.
@@ -91,20 +94,28 @@ int hn_quantize_blockwise_fp8(const void *x, int64_t rows, int64_t cols, void *q
  * xs[4]) are written into the cache q [B, cap, H, D] (strides qs[4], 1-byte
  * codes) and scale [B, cap, H, 1] (fp32, strides ss[3]) at token offset
  * `start`. One scale per (batch, token, head) row. D == 128, xs[3] == qs[3]
- * == 1. The caller guarantees start + L <= cap and finite values (the Python
- * mirror validates both, int8_kv_cache.py:128-141).
+ * == 1. start + L > cap is refused (HN_E_ARG) before anything is written, as
+ * the reference's capacity check does (int8_kv_cache.py:128-135).
+ * status: NULL (the caller guarantees finite values) or a device int32. When
+ * given, the values are validated on the device before the write, the
+ * reference's validate-before-write (int8_kv_cache.py:140-141,176) without a
+ * host synchronisation: *status is set to 0 if every value is finite, else to
+ * 1, and then nothing (codes or scales) is written. The caller reads *status
+ * after the stream reaches it.
  * Replaces _quantize_rows / quantize_kv_into, int8_kv_cache.py:22-58,125-158. */
 int hn_kv_quantize(int fmt, const void *x, const int64_t *xs, int64_t B, int64_t L,
                    int64_t H, int64_t D, void *q, const int64_t *qs, float *scale,
-                   const int64_t *ss, int64_t start, void *stream);
+                   const int64_t *ss, int64_t cap, int64_t start, int32_t *status,
+                   void *stream);
 
-/* K and V of one layer in a single launch (same shapes/strides for both).
- * Replaces quantize_kv_pair_into, int8_kv_cache.py:161-179 (after its
- * validation, which the Python mirror performs). */
+/* K and V of one layer in a single launch (same shapes/strides for both,
+ * capacity and status as in hn_kv_quantize; with a status, both K and V are
+ * validated before either is written).
+ * Replaces quantize_kv_pair_into, int8_kv_cache.py:161-179. */
 int hn_kv_quantize_pair(int fmt, const void *k, const void *v, const int64_t *xs,
                         int64_t B, int64_t L, int64_t H, int64_t D, void *qk, void *qv,
                         const int64_t *qs, float *sk, float *sv, const int64_t *ss,
-                        int64_t start, void *stream);
+                        int64_t cap, int64_t start, int32_t *status, void *stream);
 
 /* KV decode of the valid prefix: y[b,t,h,:] = bf16(decode(q[b,t,h,:]) * s[b,t,h]),
  * t < valid_len. q strides qs[4], scale strides ss[3], y bf16 strides ys[4];
@@ -141,17 +152,30 @@ int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const f
  * granularity, optionally followed by an unquantized bf16 tail (the current
  * chunk's own K/V during denoising passes).
  *   q:     bf16 [B, Lq, H, D], strides qs[4] (qs[3] == 1), D == 128
- *   kc,vc: 1-byte codes [B, cap, H, D], strides cs[4] (cs[3] == 1)
- *   ks,vs: fp32 scales [B, cap, H, 1], strides ss[3]
+ *   kc,vc: 1-byte codes [Bc, cap, H, D], strides cs[4] (cs[3] == 1)
+ *   ks,vs: fp32 scales [Bc, cap, H, 1], strides ss[3]
+ *          Bc == B, or one history slot read by every query batch (the
+ *          read-only CFG broadcast of nomas_cpt.py:547-567): cs[0] == ss[0]
+ *          == 0 (and cache_valid_stride == 0)
+ *   cache_cap: tokens the cache holds; kv_len > cache_cap is refused
  *   kv_len: cached tokens attended, positions 0 .. kv_len-1
+ *   cache_valid: NULL (every cached key valid) or bytes [Bc, >= kv_len]
+ *          with batch stride cache_valid_stride; key t of batch b takes part
+ *          iff cache_valid[b * stride + t] != 0 (the cache_mask history mask,
+ *          nomas_cpt.py:536-546)
  *   kcur,vcur: bf16 [B, cur_len, H, D] (strides curs[4]) or NULL with cur_len 0;
  *          tail token j has position kv_len + j
+ *   cur_valid: NULL or bytes [B, >= cur_len] (batch stride cur_valid_stride):
+ *          validity of the tail keys (img ones | text_mask, nomas_cpt.py:488-504)
  *   q_pos0: position of query row 0; query i has position q_pos0 + i
  *   chunk_len: key at position p is visible to query at position r iff
  *          p / chunk_len <= r / chunk_len; chunk_len <= 0 makes every key visible
+ *   softmax_scale: finite and > 0
  *   out:   bf16 [B, Lq, H, D], strides os[4]
- * O = softmax(Q K^T * softmax_scale) V with K, V dequantized as code * scale;
- * query rows that see no key are written as zeros.
+ * O = softmax(Q K^T * softmax_scale) V over the visible valid keys, with K, V
+ * the reference's dequantized values bf16(code * scale); query rows that see
+ * no key are written as zeros (range_attention.py:212-239). The probabilities
+ * multiply V as fp16 (relative rounding 2^-11) with fp32 accumulation.
  * workspace: device scratch of at least hn_attn_fp8kv_workspace_size(...)
  *        bytes (16-byte aligned; NULL/0 when that size is 0). It holds per-split
  *        partial results when the key range is split across workgroups to fill
@@ -162,10 +186,12 @@ int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const f
  * then Flex/FA3/SDPA), and flex_masked_attention, range_attention.py:212-239. */
 int hn_attn_fp8kv(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t Lq, int64_t H,
                   int64_t D, const void *kc, const void *vc, const int64_t *cs,
-                  const float *ks, const float *vs, const int64_t *ss, int64_t kv_len,
+                  const float *ks, const float *vs, const int64_t *ss, int64_t cache_cap,
+                  int64_t kv_len, const uint8_t *cache_valid, int64_t cache_valid_stride,
                   const void *kcur, const void *vcur, const int64_t *curs, int64_t cur_len,
-                  int64_t q_pos0, int64_t chunk_len, float softmax_scale, void *out,
-                  const int64_t *os, void *workspace, int64_t workspace_bytes, void *stream);
+                  const uint8_t *cur_valid, int64_t cur_valid_stride, int64_t q_pos0,
+                  int64_t chunk_len, float softmax_scale, void *out, const int64_t *os,
+                  void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Bytes of workspace hn_attn_fp8kv needs for these sizes on the current device
  * (0: none). Depends on the device's CU count. */
@@ -184,8 +210,11 @@ int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D
  * When kc is non-NULL, the rotated k and v are also written into the KV cache
  * (kc, vc codes [B, cap, H, D] with strides qs[4]; ks, vs fp32 scales with
  * strides ss[3]) at token offset start, exactly as hn_kv_quantize_pair would
- * write them (no finiteness validation: callers that need the reference's
- * validate-before-write behaviour pass kc = NULL and use hn_kv_quantize_pair).
+ * write them; start + L > cap is refused before anything is written. status
+ * (only with a cache write): NULL, or a device int32 that validates the cache
+ * write as in hn_kv_quantize: the rotated k and v are checked on the device
+ * first (same arithmetic), and if any value is NaN/Inf *status becomes 1 and
+ * the cache is not written (q and k are still rotated in place).
  * Replaces _rms_norm / _rotate_half and the q/k tail of pre_attention,
  * hymm/models/dit/modules/nomas_compile_prepost.py:18-27,49-54 (RMSNorm
  * norm_layers.py:49-63, RoPE posemb_layers.py:401-453), fused with the cache
@@ -194,7 +223,8 @@ int hn_qk_norm_rope_kv(int fmt, void *q, void *k, const void *v, const int64_t *
                        int64_t L, int64_t H, int64_t D, const void *q_weight,
                        const void *k_weight, const float *cos, const float *sin, int64_t cs,
                        float eps, void *kc, void *vc, const int64_t *qs, float *ks, float *vs,
-                       const int64_t *ss, int64_t start, void *stream);
+                       const int64_t *ss, int64_t cap, int64_t start, int32_t *status,
+                       void *stream);
 
 #ifdef __cplusplus
 }

@@ -131,6 +131,53 @@ def test_block_fused_and_validated_cache_writes_agree(dev):
         assert torch.equal(caches[0][key].view(torch.uint8), caches[1][key].view(torch.uint8)), key
 
 
+@pytest.mark.parametrize("where", ["k", "v"])
+def test_fused_cache_write_validated_on_device(dev, where):
+    """With a status word, the fused kernel's cache write is checked first on
+    the device: a NaN in k (or an Inf in v) leaves every cache byte unchanged
+    and sets the flag, while q and k are still rotated in place exactly as
+    without the cache write; finite values give flag 0 and the unchecked
+    write's bytes."""
+    print(f"case qk status {where}", flush=True)
+    ops = pkg_module("ops")
+    kvc = pkg_module("fp8_kv_cache")
+    db = pkg_module("dit_block")
+    B, L, H, D = 1, 36, 2, 128
+    g = torch.Generator(device=dev).manual_seed(41)
+    qkv = torch.randn(B, L, 3, H, D, device=dev, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(torch.bfloat16)
+    cos, sin = db.rope_tables(1, 4, 9, device=dev)
+
+    def run(x, status):
+        x = x.clone()
+        q, k, v = x.select(2, 0), x.select(2, 1), x.select(2, 2)
+        cache = kvc.make_fp8_kv_block(B, 2 * L, H, D, device=dev)
+        for buf in cache.values():
+            buf.view(torch.uint8).fill_(0x33)
+        ops.qk_norm_rope_kv_(q, k, v, w, w, cos, sin, 1e-6, cache["k"], cache["v"], cache["k_scale"],
+                             cache["v_scale"], L // 2, status)
+        return x, cache
+
+    good_x, good_cache = run(qkv, None)
+    status = torch.full((1,), 9, dtype=torch.int32, device=dev)
+    x2, cache2 = run(qkv, status)
+    assert int(status.item()) == 0
+    assert torch.equal(x2, good_x)
+    for name in good_cache:
+        assert torch.equal(cache2[name].view(torch.uint8), good_cache[name].view(torch.uint8)), name
+    bad = qkv.clone()
+    if where == "k":
+        bad[0, 7, 1, 1, 3] = float("nan")
+    else:
+        bad[0, 30, 2, 0, 100] = float("inf")
+    ref_x, _ = run(bad, None)
+    x3, cache3 = run(bad, status)
+    assert int(status.item()) == 1
+    for name, buf in cache3.items():
+        assert (buf.view(torch.uint8) == 0x33).all(), f"{name} was written"
+    assert torch.equal(x3.view(torch.int16), ref_x.view(torch.int16))   # q/k rotated regardless
+
+
 def test_qk_norm_rope_argument_errors(dev):
     ops = pkg_module("ops")
     x = torch.zeros(1, 4, 3, 2, 128, dtype=torch.bfloat16, device=dev)

@@ -168,16 +168,38 @@ def test_kv_dequantize_matches_oracle(O, dev, fmt):
     assert kvc.dequantize_kv(cache, "v", 0).shape == (B, 0, H, D)
 
 
-def test_kv_write_rejects_non_finite_before_writing(dev):
+@pytest.mark.parametrize("bad", [float("inf"), float("nan"), -float("inf")])
+def test_kv_write_rejects_non_finite_before_writing(O, dev, bad):
+    """The finiteness check runs on the GPU before the write: with a NaN/Inf
+    in V, neither K nor V (codes or scales) changes. Without a status tensor
+    the call raises ValueError as the reference does; with one it sets the
+    flag and returns without a host synchronisation."""
     kvc = pkg_module("fp8_kv_cache")
     cache = kvc.make_fp8_kv_block(1, 16, 2, 128, device=dev)
-    cache["k"].view(torch.uint8).fill_(7)
-    k = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16, device=dev)
+    for buf in cache.values():
+        buf.view(torch.uint8).fill_(7)
+    k = torch.randn(1, 4, 2, 128, device=dev).to(torch.bfloat16)
     v = k.clone()
-    v[0, 2, 1, 9] = float("inf")
+    v[0, 2, 1, 9] = bad
     with pytest.raises(ValueError, match="non-finite"):
-        kvc.quantize_kv_pair_into(cache, k, v, 0)
-    assert (u8(cache["k"]) == 7).all()
+        kvc.quantize_kv_pair_into(cache, k, v, 3)
+    for name, buf in cache.items():
+        assert (buf.view(torch.uint8) == 7).all(), f"{name} was written"
+    status = torch.full((1,), 5, dtype=torch.int32, device=dev)
+    kvc.quantize_kv_pair_into(cache, v, k, 3, status=status)      # non-finite in K this time
+    assert int(status.item()) == 1
+    for name, buf in cache.items():
+        assert (buf.view(torch.uint8) == 7).all(), f"{name} was written (deferred mode)"
+    with pytest.raises(ValueError, match="non-finite"):
+        kvc.quantize_kv_into(cache, "v", v, 0)
+    assert (u8(cache["v"]) == 7).all()
+    # finite values: status 0 and the usual bit-exact codes
+    kvc.quantize_kv_pair_into(cache, k, k, 3, status=status)
+    assert int(status.item()) == 0
+    qo, so = O.kv_quantize(bf16_bits(k))
+    assert np.array_equal(u8(cache["k"])[:, 3:7], qo) and np.array_equal(u8(cache["v"])[:, 3:7], qo)
+    assert np.array_equal(cache["k_scale"][:, 3:7].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert (u8(cache["k"])[:, :3] == 7).all() and (u8(cache["k"])[:, 7:] == 7).all()
 
 
 def test_kv_write_twice_is_deterministic(dev):
