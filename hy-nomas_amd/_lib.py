@@ -48,10 +48,15 @@ SIGNATURES = {
                       _I64, _I64, _P, _I64, _P, _P, _PI64, _I64, _P, _I64, _I64, _I64, _F, _P,
                       _PI64, _P, _I64, _P],
     "hn_attn_fp8kv_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I64],
+    "hn_attn_fp8kv_noalloc": [_I, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _PI64, _P, _P, _PI64,
+                              _I64, _I64, _P, _I64, _P, _P, _PI64, _I64, _P, _I64, _I64, _I64, _F,
+                              _P, _PI64, _P],
+    "hn_attn_fp8kv_noalloc_scratch_bytes": [],
     "hn_qk_norm_rope_kv": [_I, _P, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _F,
                            _P, _P, _PI64, _P, _P, _PI64, _I64, _I64, _P, _P],
 }
-RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64}
+RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64,
+            "hn_attn_fp8kv_noalloc_scratch_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()

@@ -36,6 +36,8 @@
 // the kv_mask of nomas_cpt.py:611-685). Tiles wholly beyond the last query's
 // chunk are never visited; tiles wholly visible to every query of the
 // workgroup skip the per-element test.
+#include <mutex>
+
 #include "hn_capi_internal.h"
 #include "hn_common.h"
 
@@ -1188,4 +1190,77 @@ extern "C" int hn_attn_fp8kv(int fmt, const void* q, const int64_t* qs, int64_t 
     HN_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))), HN_E_ARG,
                "hn_attn_fp8kv: workspace smaller than hn_attn_fp8kv_workspace_size() or misaligned");
     return attn_run(p, plan, B, Lq, workspace, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// hn_attn_fp8kv_noalloc: hn_attn_fp8kv with the split-key workspace in a
+// file-scope device array, for callers that cannot allocate. Each GPU holds
+// its own copy of `scratch` until the process ends. Host code never passes the
+// array's name (a host-side stand-in) to a kernel: the device address comes
+// from hipGetSymbolAddress, looked up once per device with that device current.
+// Every call on a device shares its scratch, so calls that overlap on one GPU
+// race; the kernels write every partial they read, so nothing needs clearing.
+// Size: a split launch keeps at most 2 workgroups per CU in one round, each
+// with 128 query rows of (128 + 2) fp32 partials, so a call needs at most
+// 2 * CUs * 128 * 130 * 4 bytes: 34.1 MB on MI355X's 256 CUs.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = 40ll << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {};
+
+static int scratch_for_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return fail(HN_E_DEVICE, "hn_attn_fp8kv_noalloc: no usable current device");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            (void)hipGetLastError();
+            set_error("hn_attn_fp8kv_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                      dev, hipGetErrorString(e));
+            return HN_E_DEVICE;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return HN_OK;
+}
+
+extern "C" int64_t hn_attn_fp8kv_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int hn_attn_fp8kv_noalloc(int fmt, const void* q, const int64_t* qs, int64_t B, int64_t Lq,
+                                     int64_t H, int64_t D, const void* kc, const void* vc,
+                                     const int64_t* cs, const float* ks, const float* vs,
+                                     const int64_t* ss, int64_t cache_cap, int64_t kv_len,
+                                     const uint8_t* cache_valid, int64_t cache_valid_stride,
+                                     const void* kcur, const void* vcur, const int64_t* curs,
+                                     int64_t cur_len, const uint8_t* cur_valid,
+                                     int64_t cur_valid_stride, int64_t q_pos0, int64_t chunk_len,
+                                     float softmax_scale, void* out, const int64_t* os,
+                                     void* stream) {
+    attn::Params p;
+    AttnPlan plan;
+    bool empty = false;
+    int rc = attn_setup(fmt, q, qs, B, Lq, H, D, kc, vc, cs, ks, vs, ss, cache_cap, kv_len, cache_valid,
+                        cache_valid_stride, kcur, vcur, curs, cur_len, cur_valid, cur_valid_stride, q_pos0,
+                        chunk_len, softmax_scale, out, os, &p, &plan, &empty);
+    if (rc != HN_OK || empty) return rc;
+    const int64_t need = plan_workspace(plan, B, Lq, H);
+    if (need > NOALLOC_SCRATCH_BYTES) {
+        set_error("hn_attn_fp8kv_noalloc: these sizes need %lld bytes of split-key scratch, more than the "
+                  "%lld the library holds per device; call hn_attn_fp8kv with a workspace",
+                  (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+        return HN_E_ARG;
+    }
+    void* ws = nullptr;
+    if (need > 0) {
+        rc = scratch_for_current_device(&ws);
+        if (rc != HN_OK) return rc;
+    }
+    return attn_run(p, plan, B, Lq, ws, (hipStream_t)stream);
 }

@@ -198,6 +198,29 @@ int hn_attn_fp8kv(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t 
 int64_t hn_attn_fp8kv_workspace_size(int64_t B, int64_t Lq, int64_t H, int64_t D,
                                      int64_t kv_len, int64_t cur_len);
 
+/* hn_attn_fp8kv without the workspace arguments: a variant that allocates
+ * nothing and takes no caller memory beyond its inputs and outputs. No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). The split-key
+ * partials go to a scratch array the library holds on each device for the life
+ * of the process, hn_attn_fp8kv_noalloc_scratch_bytes() bytes (40 MiB, above
+ * the 34.1 MB that any call needs on 256 CUs); sizes whose
+ * hn_attn_fp8kv_workspace_size() exceeds it are refused (HN_E_ARG). All
+ * calls on one device share that array, so calls that overlap on one GPU (two
+ * streams, or two threads) race. Arguments, results and errors are otherwise
+ * those of hn_attn_fp8kv. */
+int hn_attn_fp8kv_noalloc(int fmt, const void *q, const int64_t *qs, int64_t B, int64_t Lq,
+                          int64_t H, int64_t D, const void *kc, const void *vc, const int64_t *cs,
+                          const float *ks, const float *vs, const int64_t *ss, int64_t cache_cap,
+                          int64_t kv_len, const uint8_t *cache_valid, int64_t cache_valid_stride,
+                          const void *kcur, const void *vcur, const int64_t *curs, int64_t cur_len,
+                          const uint8_t *cur_valid, int64_t cur_valid_stride, int64_t q_pos0,
+                          int64_t chunk_len, float softmax_scale, void *out, const int64_t *os,
+                          void *stream);
+
+/* Bytes of the per-device scratch array of hn_attn_fp8kv_noalloc. */
+int64_t hn_attn_fp8kv_noalloc_scratch_bytes(void);
+
 /* Fused pre-attention tail of the DiT block's image stream, in place:
  *   q <- RoPE(RMSNorm_qw(q)),  k <- RoPE(RMSNorm_kw(k))
  * per (batch, token, head) row of D == 128, with the reference's op order and
