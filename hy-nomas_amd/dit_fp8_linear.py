@@ -15,15 +15,90 @@ product runs on the gfx950 FP8 matrix cores:
   * ``linear_weight(m)``    <- linear_weight (:97-100) for F.linear call sites.
   * ``fp8_linear(m, x, act)``: the fused call the FP8 block uses in place of
     ``F.linear(x, linear_weight(m), b)`` (nomas_compile_prepost.py:45-47,80-87).
+
+The reference's compiled pre/post functions receive ``linear_weight(m)`` as a
+plain tensor and call ``F.linear(x, w, b)`` on it (nomas_cpt.py:1356-1370,
+1431-1441). For an FP8StoredLinear that tensor is an ``FP8Weight``: it reports
+the bf16 [out, in] weight, turns ``F.linear`` into the fused FP8 custom op
+(``hy_nomas_amd::linear_fp8``, opaque to torch.compile), and gives every other
+operation the dequantized bf16 value the reference's dequant_weight() makes.
+FP8StoredLinear.weight returns it too, so the reference's own unchanged
+linear_weight (``module.weight`` for anything but its INT8 class) reaches the
+FP8 GEMM without a call-site edit.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.utils._pytree import tree_map
 
 from . import _lib as L
 from . import ops
+
+
+class FP8Weight(torch.Tensor):
+    """A bf16 [out, in] weight held as e4m3 codes and fp32 per-row scales.
+
+    ``F.linear(x, w, b)`` runs the per-token FP8 linear (activation quant +
+    fused GEMM with the scales and bias); x must be bf16, like the FP8
+    linear's forward. Any other operation on ``w`` sees
+    bf16(code * scale), the value dequant_weight() returns.
+    """
+
+    @staticmethod
+    def __new__(cls, codes: torch.Tensor, scale: torch.Tensor):
+        return torch.Tensor._make_wrapper_subclass(cls, codes.shape, dtype=torch.bfloat16,
+                                                   device=codes.device, requires_grad=False)
+
+    def __init__(self, codes: torch.Tensor, scale: torch.Tensor):
+        if codes.dtype != torch.float8_e4m3fn or codes.ndim != 2:
+            raise TypeError("FP8Weight holds float8_e4m3fn [out, in] codes")
+        if scale.dtype != torch.float32 or scale.numel() != codes.shape[0]:
+            raise TypeError("FP8Weight needs one fp32 scale per output row")
+        self.codes = codes
+        self.scale = scale.reshape(-1)
+
+    def __repr__(self):
+        return f"FP8Weight(shape={tuple(self.shape)}, device={self.device})"
+
+    def dequantize(self) -> torch.Tensor:
+        return (self.codes.float() * self.scale[:, None]).to(torch.bfloat16)
+
+    # torch.compile sees the two inner tensors (traceable wrapper subclass)
+    def __tensor_flatten__(self):
+        return ["codes", "scale"], None
+
+    @staticmethod
+    def __tensor_unflatten__(inner, meta, outer_size, outer_stride):
+        return FP8Weight(inner["codes"], inner["scale"])
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func is F.linear:
+            x = args[0] if args else kwargs["input"]
+            w = args[1] if len(args) > 1 else kwargs["weight"]
+            b = args[2] if len(args) > 2 else kwargs.get("bias")
+            if isinstance(w, FP8Weight) and not isinstance(x, FP8Weight):
+                return _linear_on_codes(x, w, b)
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        def value(t):
+            return t.dequantize() if isinstance(t, FP8Weight) else t
+        return func(*tree_map(value, args), **tree_map(value, kwargs or {}))
+
+
+def _linear_on_codes(x: torch.Tensor, w: FP8Weight, bias) -> torch.Tensor:
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"FP8 stored Linear requires BF16 input, got {x.dtype}")
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16)
+    y = ops.linear_fp8(x.reshape(-1, x.shape[-1]), w.codes, w.scale, bias, L.HN_ACT_NONE)
+    return y.reshape(*x.shape[:-1], w.shape[0])
 
 
 def quantize_weight(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -73,6 +148,12 @@ class FP8StoredLinear(nn.Module):
     def dequant_weight(self) -> torch.Tensor:
         return (self.weight_q.float() * self.weight_scale[:, None]).to(torch.bfloat16)
 
+    @property
+    def weight(self) -> FP8Weight:
+        """The weight as the reference's call sites take it: F.linear with it
+        runs the FP8 GEMM; anything else sees dequant_weight()."""
+        return FP8Weight(self.weight_q, self.weight_scale)
+
     def forward(self, x: torch.Tensor, act: int = L.HN_ACT_NONE) -> torch.Tensor:
         if x.dtype != torch.bfloat16:
             if (x.device.type == "cuda" and torch.is_autocast_enabled("cuda")
@@ -95,8 +176,8 @@ def fp8_linear_codes(module: "FP8StoredLinear", qx: torch.Tensor, sx: torch.Tens
 
 
 def linear_weight(module: nn.Module) -> torch.Tensor:
-    if isinstance(module, FP8StoredLinear):
-        return module.dequant_weight()
+    """The tensor the compiled pre/post functions pass to F.linear: the
+    FP8Weight of an FP8StoredLinear, else the module's own weight."""
     return module.weight
 
 

@@ -157,3 +157,135 @@ def test_load_w8_as_fp8(O, W, dev, tmp_path, layout):
     ref = O.linear_reference(qx, sx, u8(model.a.weight_q), model.a.weight_scale.cpu().numpy(),
                              O.bf16_bits_to_f32(bf16_bits(t["a.bias"])))
     assert_close_bf16(y.float().cpu().numpy(), ref, what="W8-loaded FP8 linear")
+
+
+def test_directory_layout_checks_layer_tensors(O, W, tmp_path):
+    """The directory layout's layer tensors get the same geometry check as the
+    single files (int8 [out, in] codes, fp32 [out, ceil(in/128)] scales), and
+    a missing one is a ValueError -- all before any GPU work."""
+    t = _tensors(O)
+    cases = {
+        "uint8 codes": dict(t, **{"a.weight_q": t["a.weight_q"].view(torch.uint8)}),
+        "float codes": dict(t, **{"b.weight_q": t["b.weight_q"].float()}),
+        "scale shape": dict(t, **{"a.weight_scale": torch.ones(128, 3)}),
+    }
+    for i, (what, bad) in enumerate(cases.items()):
+        root = _write_dir(W, tmp_path / f"d{i}", bad)
+        with pytest.raises(ValueError, match="shape/dtype"):
+            W.load_w8_as_fp8(Tiny, "tiny", root, "cpu")
+    missing = {k: v for k, v in t.items() if k != "b.weight_scale"}
+    root = _write_dir(W, tmp_path / "dm", missing)
+    with pytest.raises(ValueError, match="weight_scale"):
+        W.load_w8_as_fp8(Tiny, "tiny", root, "cpu")
+
+
+class TinyRope(Tiny):
+    """Tiny with a table the checkpoint omits (a non-persistent buffer, like the
+    reference's camera RoPE tables) and the method that rebuilds it."""
+
+    def __init__(self):
+        super().__init__()
+        self.register_buffer("freqs", torch.arange(16, dtype=torch.float32), persistent=False)
+
+    def rebuild_derived_buffers(self):
+        self.freqs = torch.arange(16, dtype=torch.float32) * 0.5
+
+
+class TinyRopeNoRebuild(Tiny):
+    def __init__(self):
+        super().__init__()
+        self.register_buffer("freqs", torch.arange(16, dtype=torch.float32), persistent=False)
+
+
+@pytest.mark.gpu
+def test_load_w8_rebuilds_derived_buffers(O, W, dev, tmp_path):
+    t = _tensors(O)
+    ckpt = _write_nomas(tmp_path / "n.safetensors", t)
+    model, _ = W.load_w8_as_fp8(TinyRope, "tiny", ckpt, dev)
+    assert model.freqs.device.type == "cuda" and torch.equal(model.freqs.cpu(), torch.arange(16) * 0.5)
+    with pytest.raises(ValueError, match="Unmaterialized model buffers"):
+        W.load_w8_as_fp8(TinyRopeNoRebuild, "tiny", ckpt, dev)
+    model, _ = W.load_w8_as_fp8(TinyRopeNoRebuild, "tiny", ckpt, dev,
+                                rebuild_buffers=lambda m: setattr(m, "freqs", torch.ones(16)))
+    assert torch.equal(model.freqs.cpu(), torch.ones(16))
+
+
+class _Proj(nn.Module):
+    def __init__(self, names, dims):
+        super().__init__()
+        for n, (o, i) in zip(names, dims):
+            setattr(self, n, nn.Linear(i, o, bias=False))
+
+
+class _Layer(nn.Module):
+    def __init__(self, h, f):
+        super().__init__()
+        self.mlp = _Proj(("gate_proj", "up_proj", "down_proj"), ((f, h), (f, h), (h, f)))
+        self.attn = _Proj(("q_proj", "o_proj"), ((h, h), (h, h)))
+        self.norm = nn.LayerNorm(h)
+
+
+class _Decoder(nn.Module):
+    """Stand-in for the PixelUMM decoder's layer structure (model.py:43-53)."""
+
+    def __init__(self, n=2, h=256, f=512):
+        super().__init__()
+        self.layers = nn.ModuleList(_Layer(h, f) for _ in range(n))
+
+
+def _pixelumm_file(W, dev, dec):
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator(device=dev).manual_seed(9)
+    state, names = {}, []
+    for i, layer in enumerate(dec.layers):
+        for p in W.PIXELUMM_PROJECTIONS:
+            lin = layer.get_submodule(p)
+            w = (torch.randn(lin.weight.shape, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+            q, s = pf.quantize_blockwise(w)
+            state[f"layers.{i}.{p}.fp8_weight"], state[f"layers.{i}.{p}.fp8_scale"] = q, s
+            names.append(f"decoder.layers.{i}.{p}.weight")
+        state[f"layers.{i}.norm.weight"] = torch.ones(256, dtype=torch.bfloat16, device=dev)
+    meta = dict(W.PIXELUMM_HEADER, quantized_source_keys=json.dumps(names), quantized_layers=str(len(names)))
+    return state, meta
+
+
+@pytest.mark.gpu
+def test_install_serialized_fp8(O, W, dev):
+    """PixelUMM FP8 single-file install (prequantized.py:27-65) on a stand-in
+    decoder: the serialized codes and scales are used as they are, the layers
+    compute the blockwise FP8 linear, and each rule refuses a broken input."""
+    print("case pixelumm install", flush=True)
+    pf = pkg_module("pixelumm_fp8")
+    dec = _Decoder().to(dev).to(torch.bfloat16).eval()
+    state, meta = _pixelumm_file(W, dev, dec)
+    assert W.install_serialized_fp8(dec, state, meta, "cutlass") == 10
+    assert dec._prequantized_fp8 and dec._prequantized_fp8_layers == 10
+    assert dec._prequantized_fp8_backend == "cutlass"
+    up = dec.layers[1].mlp.up_proj
+    assert isinstance(up, pf.FP8Linear) and up.fp8_weight is state["layers.1.mlp.up_proj.fp8_weight"]
+    x = torch.randn(300, 256, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y = up(x)
+    qa, sa = pf.quantize_blockwise(x)
+    ref = O.blockwise_gemm_reference(u8(qa), sa.cpu().numpy(), u8(up.fp8_weight), up.fp8_scale.cpu().numpy())
+    got = y.float().cpu().numpy()
+    rel = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    assert rel < 0.004, rel          # the reference harness's bound
+    # refusals
+    fresh = lambda: _Decoder().to(dev).to(torch.bfloat16).eval()
+    with pytest.raises(ValueError, match="metadata"):
+        W.install_serialized_fp8(fresh(), state, dict(meta, block_size="64"))
+    short = json.dumps(json.loads(meta["quantized_source_keys"])[:-1])
+    with pytest.raises(ValueError, match="manifest"):
+        W.install_serialized_fp8(fresh(), state, dict(meta, quantized_source_keys=short))
+    with pytest.raises(ValueError, match="backend"):
+        W.install_serialized_fp8(fresh(), state, meta, "deepgemm")
+    biased = fresh()
+    biased.layers[0].attn.q_proj = nn.Linear(256, 256).to(dev).to(torch.bfloat16)
+    with pytest.raises(ValueError, match="bias-free"):
+        W.install_serialized_fp8(biased, state, meta)
+    with pytest.raises(ValueError, match="BF16"):
+        W.install_serialized_fp8(fresh(), dict(state, **{"layers.0.norm.weight": torch.ones(256, device=dev)}), meta)
+    bad_scale = dict(state, **{"layers.0.mlp.gate_proj.fp8_scale": -state["layers.0.mlp.gate_proj.fp8_scale"]})
+    with pytest.raises(ValueError, match="positive"):
+        W.install_serialized_fp8(fresh(), bad_scale, meta)
