@@ -14,26 +14,35 @@ the dequantized FP8 cache followed by the current chunk's bf16 K/V.
 Each stage (pre-attention, cached attention, post-attention) is checked on the
 GPU's own inputs to that stage, at the north-star tolerance. End to end, a
 1-ulp bf16 difference at a quantizer's input flips that element's e4m3 code
-by one step (up to 12.5 %), so differences grow from stage to stage; the
-end-to-end bound below is set from that effect and stated with it."""
+by one step (up to 12.5 %), so differences grow from stage to stage. The
+end-to-end bar is therefore measured on the reference recipe itself: the CPU
+restatement's own movement when its post-attention half is fed the GPU's
+attention output (a north-star-sized difference) instead of its own. The GPU
+block must stay within that movement (times 1.5, plus the bf16 output's own
+rounding)."""
 import math
 
 import pytest
 import torch
 import torch.nn.functional as F
 
-from conftest import assert_close_bf16, pkg_module
+from conftest import assert_close_bf16, bf16_bits, pkg_module, u8
 
 pytestmark = pytest.mark.gpu
 
-# End to end, the block's update (out - img) versus the CPU restatement. At
-# width 512 the update is about 1/10 of the residual stream, so one bf16 ulp
-# of the residual is ~4 % of a typical update element; with code flips at the
-# four quantizers the measured update rel-L2 is 2.5e-2 (output 2.1e-3), while
-# each stage on identical inputs is within 2e-4 .. 5e-3. At width 3072 the
-# update is about as large as the residual: update 2.6e-2, output 2.1e-2.
-UPDATE_REL_L2 = 5e-2
+# End to end at width 512 the residual stream is about 10x the block's update,
+# so the output (img + update) meets the north-star rel-L2 directly.
 OUTPUT_REL_L2 = 1e-2
+
+
+def recipe_sensitivity(blk, img, parts, attn_gpu, attn_ref):
+    """rel-L2 by which the CPU restatement's update moves when its
+    post-attention half takes the GPU's attention output instead of its own:
+    the code flips the reference recipe itself makes for that difference."""
+    x = _cpu(img).float()
+    a = ref_post(blk, img, attn_gpu, parts).float() - x
+    b = ref_post(blk, img, attn_ref, parts).float() - x
+    return _rel(a, b)
 
 
 def _fake_quant_rows(x):
@@ -42,13 +51,15 @@ def _fake_quant_rows(x):
     return (x / s).to(torch.float8_e4m3fn).float() * s
 
 
-def _ref_linear(m, x, gelu=False):
-    """FP8 linear on bf16 x: fp32 accumulate of e4m3 x e4m3 with scales, + bias, bf16 out."""
+def _ref_linear(m, x, gelu=False, fp32=False):
+    """FP8 linear on bf16 x: fp32 accumulate of e4m3 x e4m3 with scales, + bias,
+    bf16 out (fp32: the value before that rounding)."""
     w = m.weight_q.float().cpu() * m.weight_scale.float().cpu().reshape(-1, 1)
     y = _fake_quant_rows(x.float().reshape(-1, x.shape[-1])) @ w.T + m.bias.float().cpu()
     if gelu:
         y = F.gelu(y, approximate="tanh")
-    return y.to(torch.bfloat16).reshape(*x.shape[:-1], -1)
+    y = y.reshape(*x.shape[:-1], -1)
+    return y if fp32 else y.to(torch.bfloat16)
 
 
 def _modulate(x, shift, scale):
@@ -154,12 +165,8 @@ def test_block_stages_match_reference(dev):
             assert_close_bf16(_cpu(got).float().numpy(), want.float().numpy(), what=f"pre-attention {name}")
         attn = ca.chunk_attention(q, cache, hist, k_cur=k, v_cur=v)
         ra = ref_attention(q, k, v, hk, hv)
-        # probabilities enter PV rounded to bf16, as in the reference's flash
-        # attention: allowance 2^-8 * sum p |v| / l (the same weights over |V|)
-        env = ref_attention(q, k, v.abs(), hk, hv.abs())
         print(f"attention rel-L2 {_rel(attn.float(), ra):.3e}", flush=True)
-        assert_close_bf16(_cpu(attn).float().numpy(), ra.numpy(), what="cached attention",
-                          extra=2.0 ** -8 * env.numpy())
+        assert_close_bf16(_cpu(attn).float().numpy(), ra.numpy(), what="cached attention")
         out = blk.post_attention(img, attn, parts)
         ro = ref_post(blk, img, attn, parts)
         upd, rupd = _cpu(out).float() - _cpu(img).float(), ro.float() - _cpu(img).float()
@@ -172,15 +179,22 @@ def test_block_stages_match_reference(dev):
 def test_block_end_to_end(dev, update_cache):
     print(f"case dit block end to end update_cache={update_cache}", flush=True)
     blk, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev)
+    ca = pkg_module("cache_attention")
     with torch.no_grad():
         out = blk(img, vec, cos, sin, cache, hist, update_cache=update_cache)
         rq, rk, rv, rparts = ref_pre(blk, img, vec, cos, sin)
-        ro = ref_post(blk, img, ref_attention(rq, rk, rv, hk, hv), rparts)
+        ra = ref_attention(rq, rk, rv, hk, hv)
+        ro = ref_post(blk, img, ra, rparts)
+        q, k, v, parts = blk.pre_attention(img, vec, cos, sin)
+        ga = ca.chunk_attention(q, cache, hist, k_cur=k, v_cur=v)
     got, want, x = _cpu(out).float(), ro.float(), _cpu(img).float()
     rel_upd, rel_out = _rel(got - x, want - x), _rel(got, want)
-    print(f"block update rel-L2 {rel_upd:.3e}, output rel-L2 {rel_out:.3e}", flush=True)
+    sens = recipe_sensitivity(blk, img, rparts, ga, ra)
+    print(f"block update rel-L2 {rel_upd:.3e} (recipe sensitivity {sens:.3e}), "
+          f"output rel-L2 {rel_out:.3e}", flush=True)
     assert torch.isfinite(got).all()
-    assert rel_out <= OUTPUT_REL_L2 and rel_upd <= UPDATE_REL_L2
+    assert rel_out <= OUTPUT_REL_L2
+    assert rel_upd <= 1.5 * sens + 2.0 ** -8
     written = cache["k"][:, hist:hist + L].view(torch.uint8)
     assert bool(written.any()) == update_cache
     assert not cache["k"][:, hist + L:].view(torch.uint8).any()
@@ -200,18 +214,26 @@ def test_block_end_to_end_full_width(dev):
     quantizer, K 3072 and 12288 GEMMs (persistent kernel) and the 12288-column
     row quantizer of fc2's input, against the CPU restatement."""
     print("case dit block end to end full width", flush=True)
+    ca = pkg_module("cache_attention")
     blk, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev, hidden=3072, heads=24)
     with torch.no_grad():
         out = blk(img, vec, cos, sin, cache, hist, update_cache=False)
         rq, rk, rv, rparts = ref_pre(blk, img, vec, cos, sin)
-        ro = ref_post(blk, img, ref_attention(rq, rk, rv, hk, hv), rparts)
+        ra = ref_attention(rq, rk, rv, hk, hv)
+        ro = ref_post(blk, img, ra, rparts)
+        q, k, v, parts = blk.pre_attention(img, vec, cos, sin)
+        ga = ca.chunk_attention(q, cache, hist, k_cur=k, v_cur=v)
     got, want, x = _cpu(out).float(), ro.float(), _cpu(img).float()
     rel_upd, rel_out = _rel(got - x, want - x), _rel(got, want)
-    print(f"full-width block update rel-L2 {rel_upd:.3e}, output rel-L2 {rel_out:.3e}", flush=True)
+    sens = recipe_sensitivity(blk, img, rparts, ga, ra)
+    print(f"full-width block update rel-L2 {rel_upd:.3e} (recipe sensitivity {sens:.3e}), "
+          f"output rel-L2 {rel_out:.3e}", flush=True)
     assert torch.isfinite(got).all()
-    # the update is about as large as the residual here, so the output carries
-    # the update's relative error
-    assert rel_upd <= UPDATE_REL_L2 and rel_out <= UPDATE_REL_L2
+    # Here the update is about as large as the residual, so the output carries
+    # the update's relative error; both stay within what the recipe itself
+    # moves for the attention's north-star-sized difference.
+    assert rel_upd <= 1.5 * sens + 2.0 ** -8
+    assert rel_out <= 1.5 * sens + 2.0 ** -8
 
 
 def test_block_fused_ln_quant_matches_unfused(dev):
@@ -272,3 +294,251 @@ def test_ar_chunk_loop_structure(dev):
     z1 = m3.generate_chunk(noise[1], vecs[:3], vecs[3], sig)
     assert not torch.equal(x1, z1)                              # history changes the result
     assert torch.isfinite(x1).all()
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 4 at its own size, and the AR loop (config 5)
+
+def _ref_pre_rows(blk, img, vec, cos, sin, rows):
+    """ref_pre restricted to token rows (every op but RoPE's table is per row);
+    also returns v before its bf16 rounding."""
+    img, vec = _cpu(img)[:, rows], _cpu(vec)
+    n, C = img.shape[1], img.shape[2]
+    H, D = blk.heads, blk.head_dim
+    parts = F.linear(F.silu(vec), _cpu(blk.mod.weight), _cpu(blk.mod.bias)).chunk(6, dim=-1)
+    x = _modulate(F.layer_norm(img, (C,), eps=1e-6), parts[0], parts[1])
+    qkv32 = _ref_linear(blk.qkv, x, fp32=True)
+    q, k, v = qkv32.to(torch.bfloat16).view(1, n, 3, H, D).unbind(2)
+    q = _rms_norm(q, _cpu(blk.q_norm), 1e-6).to(v)
+    k = _rms_norm(k, _cpu(blk.k_norm), 1e-6).to(v)
+    c = _cpu(cos)[rows].view(1, n, 1, D)
+    s = _cpu(sin)[rows].view(1, n, 1, D)
+    q = (q.float() * c + _rotate_half(q) * s).type_as(v)
+    k = (k.float() * c + _rotate_half(k) * s).type_as(v)
+    return q, k, v, parts, qkv32.view(1, n, 3, H, D)[:, :, 2]
+
+
+def test_config4_block_at_full_size_sampled_rows(O, dev):
+    """one block at hidden 3072, 24 heads, FFN 12288 on a
+    10800-token chunk (3 x 45 x 80 RoPE) over a 75 600-token (7-chunk) FP8
+    cache. Each stage runs at full size on the GPU -- QKV N = 9216, fc2 K =
+    12288 at M = 10800, the 12288-column row quantizer, the 8-wave attention
+    -- and is checked on its GPU inputs for 64 sampled token rows, all heads,
+    at max-abs 2e-2 / rel-L2 1e-2. The post-attention half holds three
+    quantizers of its own, so it is checked step by step on the block's own
+    intermediates (rebuilt with the same ops and shown to reproduce the
+    block's output bit for bit): every quantizer's codes bit-exact against the
+    oracle, every GEMM against the fp64 dequantize-then-matmul of its codes,
+    the residual adds within one bf16 ulp of the reference's bf16 ops."""
+    print("case config-4 block full size", flush=True)
+    db = pkg_module("dit_block")
+    ca = pkg_module("cache_attention")
+    kvc = pkg_module("fp8_kv_cache")
+    H, D, C, chunk, n_hist = 24, 128, 3072, 10800, 7
+    g = torch.Generator(device=dev).manual_seed(40)
+    blk = db.FP8DiTBlock(C, H, device=dev, generator=g)
+    hist = n_hist * chunk
+    cache = kvc.make_fp8_kv_block(1, hist + chunk, H, D, device=dev)
+    for c in range(n_hist):
+        gain = torch.empty(H, device=dev).uniform_(0.5, 4.0, generator=g)
+        k = (torch.randn(1, chunk, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        v = (torch.randn(1, chunk, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+        kvc.quantize_kv_pair_into(cache, k, v, c * chunk)
+    del k, v
+    img = torch.randn(1, chunk, C, device=dev, generator=g).to(torch.bfloat16)
+    vec = torch.randn(1, C, device=dev, generator=g).to(torch.bfloat16)
+    cos, sin = db.rope_tables(3, 45, 80, t_offset=3 * n_hist, device=dev)
+    rows = torch.cat([torch.arange(0, 16), torch.arange(5392, 5408), torch.arange(10768, 10800)])
+    with torch.no_grad():
+        q, k, v, parts = blk.pre_attention(img, vec, cos, sin)
+        attn = ca.chunk_attention(q, cache, hist, k_cur=k, v_cur=v)
+        out = blk.post_attention(img, attn, parts)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    torch.set_grad_enabled(False)   # the CPU restatement reads the modules' parameters
+    # pre-attention on the sampled rows: v against the linear's fp32 value;
+    # q and k against the reference's bf16 RMSNorm + RoPE results (one bf16 ulp)
+    rq, rk, rv, _, rv32 = _ref_pre_rows(blk, img, vec, cos, sin, rows)
+    assert_close_bf16(_cpu(v)[:, rows].float().numpy(), rv32.numpy(), what="config-4 v")
+    for name, got, want in (("q", q, rq), ("k", k, rk)):
+        assert_close_bf16(_cpu(got)[:, rows].float().numpy(), want.float().numpy(), what=f"config-4 {name}",
+                          ref_is_bf16=True)
+    # attention of the sampled queries over [decoded history | this chunk's bf16 K/V]
+    hk = (cache["k"][:, :hist].float() * cache["k_scale"][:, :hist]).to(torch.bfloat16).float().cpu()
+    hv = (cache["v"][:, :hist].float() * cache["v_scale"][:, :hist]).to(torch.bfloat16).float().cpu()
+    ra = ref_attention(_cpu(q)[:, rows], k, v, hk, hv)
+    del hk, hv
+    assert_close_bf16(_cpu(attn)[:, rows].float().numpy(), ra.numpy(), what="config-4 attention")
+    torch.set_grad_enabled(True)
+    _check_post_steps(O, blk, img, attn, parts, out, rows)
+
+
+def _check_post_steps(O, blk, img, attn, parts, out, rows):
+    """The block's post-attention half step by step on the given token rows."""
+    import numpy as np
+    ops = pkg_module("ops")
+    L_ = pkg_module("_lib")
+    B, L, C = img.shape
+    bias = lambda m: m.bias.detach().to(torch.bfloat16)
+    with torch.no_grad():
+        qa, sa = ops.quantize_rows_fp8(attn.reshape(-1, C))
+        y1 = ops.gemm_fp8_rowcol(qa, blk.proj.weight_q, sa, blk.proj.weight_scale, bias(blk.proj), 0)
+        x1 = img + y1.view(B, L, C) * parts[2].unsqueeze(1)
+        qh, sh = ops.ln_modulate_quantize_fp8(x1, parts[3], parts[4], 1e-6)
+        h = ops.gemm_fp8_rowcol(qh, blk.fc1.weight_q, sh, blk.fc1.weight_scale, bias(blk.fc1), L_.HN_ACT_GELU_TANH)
+        q2, s2 = ops.quantize_rows_fp8(h)
+        y2 = ops.gemm_fp8_rowcol(q2, blk.fc2.weight_q, s2, blk.fc2.weight_scale, bias(blk.fc2), 0)
+        out2 = x1 + y2.view(B, L, C) * parts[5].unsqueeze(1)
+    assert torch.equal(out2, out), "rebuilt post-attention differs from the block's"
+    r = rows.numpy()
+    f32 = O.bf16_bits_to_f32
+
+    def codes_exact(q, s, ref, what):
+        assert np.array_equal(u8(q)[r], ref[0]), f"{what}: codes differ from the oracle"
+        assert np.array_equal(s.cpu().numpy()[r].view(np.uint32), ref[1].view(np.uint32)), f"{what}: scales"
+
+    def gemm_close(y, q, s, m, gelu, what):
+        ref = O.linear_reference(u8(q)[r], s.cpu().numpy()[r], u8(m.weight_q), m.weight_scale.cpu().numpy(),
+                                 f32(bf16_bits(bias(m))), gelu=gelu)
+        assert_close_bf16(y.float().cpu().numpy()[r], ref, what=what)
+
+    codes_exact(qa, sa, O.quantize_rows_fp8(bf16_bits(attn.reshape(-1, C))[r]), "out-proj input quant")
+    gemm_close(y1, qa, sa, blk.proj, False, "out-proj GEMM")
+    ref_x1 = (_cpu(img)[:, rows] + _cpu(y1).view(B, L, C)[:, rows] * _cpu(parts[2]).unsqueeze(1)).float()
+    assert_close_bf16(_cpu(x1)[:, rows].float().numpy(), ref_x1.numpy(), what="residual 1", ref_is_bf16=True)
+    ln_ref = O.ln_modulate_quantize_fp8(bf16_bits(x1[0])[r], bf16_bits(parts[3]), bf16_bits(parts[4]), 1e-6)
+    codes_exact(qh, sh, ln_ref, "LayerNorm + modulate + quant")
+    gemm_close(h, qh, sh, blk.fc1, True, "fc1 GEMM + GELU")
+    codes_exact(q2, s2, O.quantize_rows_fp8(bf16_bits(h)[r]), "fc2 input quant (12288 columns)")
+    gemm_close(y2, q2, s2, blk.fc2, False, "fc2 GEMM (K 12288)")
+    ref_out = (_cpu(x1)[:, rows] + _cpu(y2).view(B, L, C)[:, rows] * _cpu(parts[5]).unsqueeze(1)).float()
+    assert_close_bf16(_cpu(out)[:, rows].float().numpy(), ref_out.numpy(), what="residual 2", ref_is_bf16=True)
+
+
+def _ref_ar_chunk(blocks, caches, valid, x, vecs, vec_write, sigmas, cos, sin, O):
+    """CPU restatement of FP8ARModel.generate_chunk (causal_ar.py:2348-2432,
+    2624-2645): Euler updates over the denoising passes, each pass running
+    the blocks over [decoded history | this chunk], then a write pass whose
+    K/V go through the KV-write recipe. History comes from the GPU cache
+    bytes (pinned separately against the oracle). Returns the final latent
+    and each block's written bf16 (K, V)."""
+    def dq(c, key):
+        return (c[key][:, :valid].float() * c[key + "_scale"][:, :valid]).to(torch.bfloat16).float().cpu()
+
+    hists = [(dq(c, "k"), dq(c, "v")) for c in caches]
+
+    def run(img, vec, write):
+        kv = []
+        for blk, (hk, hv) in zip(blocks, hists):
+            q, k, v, parts = ref_pre(blk, img, vec, cos, sin)
+            if write:
+                kv.append((k, v))
+            img = ref_post(blk, img, ref_attention(q, k, v, hk, hv), parts)
+        return img, kv
+
+    x = _cpu(x)
+    for i, vec in enumerate(vecs):
+        v_pred, _ = run(x, vec, False)
+        x = x + (sigmas[i + 1] - sigmas[i]) * v_pred
+    _, kv = run(x, vec_write, True)
+    return x, kv
+
+
+def test_ar_loop_against_cpu_restatement(O, dev):
+    """Two chunks of a 2-block, hidden-256 model against the CPU restatement of
+    the loop: per chunk 3 Euler denoising passes and one write pass at the
+    chunk's RoPE offset, then the valid length advances. The latents agree
+    within 2e-2 rel-L2, and each layer's written cache rows, decoded, hold
+    the restatement's write-pass K/V up to e4m3 rounding: per element at most
+    2^-4 relative of the row's scale grid, about 2.5e-2 rel-L2 in all (the
+    codes themselves are bit-exact for given inputs, pinned by the KV-write
+    tests; here the inputs differ by the chunk's bf16 roundings, which moves
+    codes near their rounding boundaries)."""
+    print("case ar loop parity", flush=True)
+    db = pkg_module("dit_block")
+    kw = dict(depth=2, hidden=256, heads=2, latent_shape=(1, 4, 5), max_chunks=3, device=dev)
+    m = db.FP8ARModel(seed=11, **kw)
+    L = m.tokens_per_chunk
+    g = torch.Generator(device=dev).manual_seed(12)
+    sig = torch.linspace(1.0, 0.0, 4).tolist()
+    for chunk in range(2):
+        noise = torch.randn(1, L, 256, device=dev, generator=g).to(torch.bfloat16)
+        vecs = [torch.randn(1, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+        valid, frames = m.cache_valid_len, m.frames_done
+        cos, sin = db.rope_tables(1, 4, 5, t_offset=frames, device=dev)
+        rx, rw = _ref_ar_chunk(m.blocks, m.caches, valid, noise, vecs[:3], vecs[3], sig, cos, sin, O)
+        with torch.no_grad():
+            x = m.generate_chunk(noise, vecs[:3], vecs[3], sig)
+        assert m.cache_valid_len == valid + L and m.frames_done == frames + 1
+        rel = _rel(x.float(), rx.float())
+        print(f"chunk {chunk}: latent rel-L2 {rel:.3e}", flush=True)
+        assert torch.isfinite(x.float()).all() and rel <= 2e-2
+        for layer, (cache, (rk, rv)) in enumerate(zip(m.caches, rw)):
+            for name, want in (("k", rk), ("v", rv)):
+                dec = (cache[name][:, valid:valid + L].float()
+                       * cache[name + "_scale"][:, valid:valid + L]).cpu()
+                r = _rel(dec, want.float())
+                print(f"  layer {layer} {name}: decoded cache vs restated K/V rel-L2 {r:.3e}", flush=True)
+                assert r <= 4e-2, (layer, name, r)
+
+
+def test_config5_ar_chunk_at_full_size(dev):
+    """BASELINE config 5 at full size: 40 blocks (hidden 3072, 24 heads) over
+    16 prior 10800-token chunks, 4 denoising passes + 1 write pass. The
+    latent is finite; a second run of the same chunk is bit-identical; the
+    denoising passes leave every cache unchanged; the write pass changes each
+    layer's cache only in [valid, valid + 10800); valid length and frame
+    count advance. (Cache contents are compared through checksums.)"""
+    print("case config-5 AR chunk full size", flush=True)
+    db = pkg_module("dit_block")
+    ops = pkg_module("ops")
+    depth, prior, L = 40, 16, 10800
+    m = db.FP8ARModel(depth=depth, device=dev, seed=7)
+    g = torch.Generator(device=dev).manual_seed(99)
+    k = torch.randn(1, L, 24, 128, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, L, 24, 128, device=dev, generator=g).to(torch.bfloat16)
+    for cache in m.caches:
+        for buf in cache.values():
+            buf.view(torch.uint8).fill_(0x5A)          # sentinel beyond the history
+        for c in range(prior):
+            ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"], cache["v_scale"], k, v, c * L)
+    del k, v
+    valid = prior * L
+    m.cache_valid_len, m.frames_done = valid, prior * 3
+    noise = torch.randn(1, L, 3072, device=dev, generator=g).to(torch.bfloat16)
+    vecs = [torch.randn(1, 3072, device=dev, generator=g).to(torch.bfloat16) for _ in range(5)]
+    sig = torch.linspace(1.0, 0.0, 5).tolist()
+
+    def sums(lo, hi):
+        """Per layer, an int64 checksum of the K/V codes and scales in token rows [lo, hi)."""
+        out = []
+        for c in m.caches:
+            s = 0
+            for key in ("k", "v", "k_scale", "v_scale"):
+                b = c[key][:, lo:hi].contiguous().view(torch.uint8).to(torch.int64)
+                s += int((b * (torch.arange(b.numel(), device=dev, dtype=torch.int64).view(b.shape) % 251 + 1)).sum())
+            out.append(s)
+        return out
+
+    before_hist, before_tail = sums(0, valid), sums(valid + L, m.capacity)
+    sentinel_chunk = sums(valid, valid + L)
+    with torch.no_grad():
+        for vec in vecs[:4]:                              # the denoising passes alone
+            m.forward_chunk(noise, vec, update_cache=False)
+    torch.cuda.synchronize()
+    assert sums(0, valid) == before_hist and sums(valid + L, m.capacity) == before_tail
+    assert sums(valid, valid + L) == sentinel_chunk
+    with torch.no_grad():
+        x1 = m.generate_chunk(noise, vecs[:4], vecs[4], sig)
+    torch.cuda.synchronize()
+    assert m.cache_valid_len == valid + L and m.frames_done == prior * 3 + 3
+    assert torch.isfinite(x1.float()).all()
+    assert sums(0, valid) == before_hist and sums(valid + L, m.capacity) == before_tail
+    written = sums(valid, valid + L)
+    assert all(w != s for w, s in zip(written, sentinel_chunk)), "a layer's chunk was not written"
+    # the same chunk again: bit-identical latent and cache bytes
+    m.cache_valid_len, m.frames_done = valid, prior * 3
+    with torch.no_grad():
+        x2 = m.generate_chunk(noise, vecs[:4], vecs[4], sig)
+    assert torch.equal(x1, x2)
+    assert sums(valid, valid + L) == written
