@@ -27,6 +27,7 @@
 
 #include "hn_capi_internal.h"
 #include "hn_common.h"
+#include "gemm_dma.h"
 
 namespace hn {
 namespace gemm {
@@ -73,7 +74,6 @@ struct Params {
 // logical chunk, and with 128-byte rows the bank group of (r, c) is
 // 8 (r & 1) + position, so the swizzle must spread rows of equal parity --
 // hence (r >> 1), not r.
-HN_DEVICE int swz_pos(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 HN_DEVICE int swz(int row, int chunk) { return row * BK + (swz_pos(row, chunk) << 4); }
 
 // Direct global -> LDS loads of one operand tile (global_load_lds_dwordx4:
@@ -138,13 +138,6 @@ struct Frags {
     i32x8 b[4];
     i32x8 a[4];
 };
-
-HN_DEVICE void read_frags(Frags& f, const uint8_t* st, int kh, int wm, int wn, int lane) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f.b[i] = read_frag(st + TILE_BYTES, wn * 128 + i * 32 + (lane & 31), kh, lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.a[j] = read_frag(st, wm * 128 + j * 32 + (lane & 31), kh, lane);
-}
 
 HN_DEVICE void mfma_slice(f32x16 (&acc)[4][4], const Frags& f) {
 #pragma unroll
@@ -315,44 +308,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    if (MODE == ROWCOL) {
-        // Software pipeline over K slices of 64 bytes (two per 128-byte stage).
-        // Phase A of step kt: MFMAs on slice 0 of stage kt while slice 1's
-        // fragments stream in from LDS. Then one wait + barrier: the DMA of
-        // stage kt+1 has landed and every wave is done reading stage kt, which
-        // immediately starts receiving step kt+2. Phase B: MFMAs on slice 1
-        // while slice 0 of stage kt+1 streams in.
-        uint8_t* const st0 = smem;
-        uint8_t* const st1 = smem + STAGE_BYTES;
-        load_tile_lds(st0, p.a, m0, p.M, p.K, 0, wave, lane);
-        load_tile_lds(st0 + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
-        if (KT > 1) {
-            load_tile_lds(st1, p.a, m0, p.M, p.K, BK, wave, lane);
-            load_tile_lds(st1 + TILE_BYTES, p.b, n0, p.N, p.K, BK, wave, lane);
-            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // stage 0 (issued first) landed
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        __syncthreads();
-        Frags f0, f1;
-        read_frags(f0, st0, 0, wm, wn, lane);
-        for (int kt = 0; kt < KT; ++kt) {
-            uint8_t* cur = (kt & 1) ? st1 : st0;
-            uint8_t* nxt = (kt & 1) ? st0 : st1;
-            read_frags(f1, cur, 1, wm, wn, lane);
-            mfma_slice(acc, f0);
-            interleave_reads_with_mfma();
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (kt + 2 < KT) {
-                load_tile_lds(cur, p.a, m0, p.M, p.K, (int64_t)(kt + 2) * BK, wave, lane);
-                load_tile_lds(cur + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 2) * BK, wave, lane);
-            }
-            if (kt + 1 < KT) read_frags(f0, nxt, 0, wm, wn, lane);
-            mfma_slice(acc, f1);
-            interleave_reads_with_mfma();
-        }
-    } else {
     load_tile_lds(smem, p.a, m0, p.M, p.K, 0, wave, lane);
     load_tile_lds(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
@@ -367,20 +322,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
         }
         const uint8_t* lA = cur;
         const uint8_t* lB = cur + TILE_BYTES;
-        if (MODE == ROWCOL) {
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                i32x8 fb[4], fa[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) fb[i] = read_frag(lB, wn * 128 + i * 32 + (lane & 31), kh, lane);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) fa[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), kh, lane);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
-            }
-        } else {
+        {
             // Promote this 128-wide K block with its own scale. The wave's
             // 128 x 128 sub-tile lies inside one 128 x 128 scale block of
             // each operand, so the factor is uniform over the wave.
@@ -407,7 +349,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-    }
     }
 
     epilogue<MODE>(acc, p, m0, n0, smem, wave, wm, wn, lane);
@@ -941,34 +882,16 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         // A 192-wide tile still fills all 256 stage rows; rows past its width
         // are clamped like rows past N (never read by an MFMA).
         const int64_t b_rows = p.N - n0_ < TBN ? p.N - n0_ : TBN;
-        a_lim = (uint32_t)((a_rows - 1) * p.K + 112);
-        b_lim = (uint32_t)((b_rows - 1) * p.K + 112);
+        a_lim = dma_limit(a_rows, p.K);
+        b_lim = dma_limit(b_rows, p.K);
     };
-    // Per-lane DMA geometry from a regenerated lane id l: the lane's row in
-    // load 0, its chunk offsets for even and odd loads, and row K.
-    struct DmaLane {
-        int row;
-        uint32_t chunk[2];
-        uint32_t rowk;  // row * K
-    };
-    auto dma_lane = [&](int l) {
-        DmaLane d;
-        d.row = wave * 64 + (l >> 3);
-        d.chunk[0] = (uint32_t)swz_pos(d.row, l & 7) << 4;
-        d.chunk[1] = (uint32_t)swz_pos(d.row + 8, l & 7) << 4;
-        d.rowk = (uint32_t)d.row * (uint32_t)p.K;
-        return d;
-    };
-    // Offset of load q: row K + chunk + 8 q K (8 q K wave-uniform), capped
-    // at the source tile's limit. A row r <= last keeps its offset
-    // (r K + chunk <= last K + 112, chunk <= 112); a row past the operand's
-    // end starts at >= (last + 1) K >= last K + 128 and reads the last
-    // chunk of the last row's window instead (never used). Every load of
-    // every wave stays inside the operand, whichever rows the wave itself
-    // multiplies.
-    auto dma_off = [&](const DmaLane& d, int q, uint32_t lim) {
-        return min(d.rowk + d.chunk[q & 1] + (uint32_t)(8 * q) * (uint32_t)p.K, lim);
-    };
+    // Per-lane DMA geometry from a regenerated lane id l (gemm_dma.h: the
+    // lane's row in load 0, its chunk offsets for even and odd loads, row K),
+    // and the offset of load q capped at the source tile's limit, so every
+    // load of every wave stays inside the operand, whichever rows the wave
+    // itself multiplies.
+    auto dma_lane = [&](int l) { return dma_lane_of(wave, l, p.K); };
+    auto dma_off = [&](const DmaLane& d, int q, uint32_t lim) { return dma_offset(d, q, p.K, lim); };
     // Current tile: origin and blocks inside the matrix (imax weight blocks of
     // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
     // 32 rows). Wave-uniform. Tiles with every block inside the matrix take
