@@ -10,8 +10,8 @@ synthetic workload with inputs resident in HBM:
 ms / GB/s and the KV-write GB/s ride along in the same JSON line, as does the
 config-1 linear. Timing uses HIP events on the stream the kernels run on.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--only all|linear|kv|attn|copy]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-seconds S]
+                       [--no-cpu-baseline] [--no-ar] [--only all|linear|kv|attn|copy|ar]
 ``--only`` runs one workload (for per-kernel counter passes); ``copy`` is a
 plain 1 GiB device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
 """
@@ -21,6 +21,7 @@ import argparse
 import importlib
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -58,6 +59,19 @@ def attn_unique_bytes(h, lq, lk, d):
     return h * lq * d * 2 * 2 + 2 * h * lk * d + 2 * h * lk * 4   # Q + O bf16, K/V codes, scales
 
 
+def clock_settle(fn, seconds, torch):
+    """Run fn back to back for a fixed wall-clock time (synchronizing every
+    16 calls), so that the timed loops start at the GPU's steady clock."""
+    calls, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(16):
+            fn()
+        calls += 16
+        torch.cuda.synchronize()
+    return {"seconds": round(time.perf_counter() - t0, 3), "calls": calls,
+            "workload": "north-star FP8 linear, back to back, before any timed loop"}
+
+
 def time_loop(fn, steps, warmup, stream=None):
     import torch
     for _ in range(warmup):
@@ -77,14 +91,15 @@ def time_loop(fn, steps, warmup, stream=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 100 timed steps after 50 warmup steps: the north-star linear is ~0.4 ms,
-    # and 20 steps after 5 warmup fell inside the clock transient of a GPU
-    # coming out of idle (the same GEMM's calls drift from 410 to 510 us and
-    # back within the first ~30 calls), reading 15 % low.
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
+    # A GPU coming out of idle runs the first few hundred ms of dense FP8 work
+    # at a moving clock (the north-star GEMM's calls drift from ~0.38 to
+    # ~0.5 ms and back within the first ~30 calls); a fixed-length settle
+    # phase of that same work precedes every timed workload, whatever
+    # --warmup is, and is reported in the JSON line.
+    ap.add_argument("--settle-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
     ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "copy", "ar"])
     args = ap.parse_args()
@@ -127,6 +142,8 @@ def main():
     del w
     qx, sx = ops.quantize_rows_fp8(x)
 
+    settle = clock_settle(lambda: ops.linear_fp8(x, qw, sw, bias, 1), args.settle_seconds, torch)
+    log(f"clock settle: {settle['calls']} north-star linear calls in {settle['seconds']:.2f} s")
     ms_linear = time_loop(lambda: ops.linear_fp8(x, qw, sw, bias, 1), args.steps, args.warmup)
     ms_gemm = time_loop(lambda: ops.gemm_fp8_rowcol(qx, qw, sx, sw, bias, 1), args.steps, args.warmup)
     # The short kernels are timed through the C ABI with preallocated outputs:
@@ -204,10 +221,10 @@ def main():
     # ---------------- config 5: 40-block AR chunk at the largest cache
     ar_res = bench_ar(args, torch, ops, dev, log) if not args.no_ar else None
 
-    # ---------------- CPU baseline: the oracle's dequantize-then-matmul
+    # ---------------- CPU baseline: the reference's own torch CPU paths
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(args.cpu_seconds, log)
+        cpu = cpu_baseline(log)
 
     result = {
         "metric": "FP8 linear TFLOP/s (% MFMA peak); FP8-KV chunk attn ms + HBM GB/s",
@@ -236,7 +253,11 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
             "traffic": gemm_traffic_bytes(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over this GEMM "
+                              "(profiles/fp8_gemm_north_star_traffic.json), scaled by the same counters "
+                              "over a 1 GiB copy; not measured inside this run",
         },
+        "clock_settle": settle,
         "linear": {"ms": round(ms_linear, 4), "tflops": round(linear_tflops, 2),
                    "frac_fp8_peak": round(linear_tflops / FP8_PEAK_TFLOPS, 4),
                    "gemm_ms": round(ms_gemm, 4), "act_quant_us": round(ms_quant * 1e3, 2),
@@ -377,103 +398,152 @@ def gemm_traffic_bytes():
         return None
 
 
-def cpu_baseline(seconds, log):
-    """Oracle dequantize-then-matmul of a row sample of the north-star linear on
-    the host's cores: per-token quant in C (1 thread), dequant + float64 BLAS matmul."""
-    import numpy as np
-    from threadpoolctl import threadpool_info, threadpool_limits
-    from oracle import oracle as O
+def _median_seconds(fn, reps=5, warmup=2):
+    """Median wall time of ``reps`` calls of fn after ``warmup`` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
 
-    cores = min(16, os.cpu_count() or 1)
-    rng = np.random.default_rng(0)
-    rows = 256
-    x = rng.standard_normal((rows, NS_K)).astype(np.float32)
-    w = (rng.standard_normal((NS_N, NS_K)) * 0.02).astype(np.float32)
-    xb = O.f32_to_bf16_bits(x)
-    qw, sw = O.quantize_rows_fp8(O.f32_to_bf16_bits(w))
-    bias = rng.standard_normal(NS_N) * 0.01
-    with threadpool_limits(limits=cores, user_api="blas"):
-        blas = [i.get("num_threads") for i in threadpool_info() if i.get("user_api") == "blas"]
-        n, t0 = 0, time.perf_counter()
-        while True:
-            qx, sx = O.quantize_rows_fp8(xb)
-            O.linear_reference(qx, sx, qw, sw, bias, gelu=True)
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or n >= 50:
-                break
-    tflops = gemm_flops(rows, NS_K, NS_N) * n / el / 1e12
-    log(f"cpu baseline {tflops * 1e3:.2f} GFLOP/s over {n} x {rows} rows in {el:.1f} s")
-    out = {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": int(blas[0]) if blas else cores,
-           "kind": "port",
-           "sample": f"{n} x {rows} token rows of the north-star linear ({rows}x{NS_K}x{NS_N}): "
-                     f"oracle per-token e4m3 quant (C) + dequantize-then-matmul (numpy float64 BLAS) "
-                     f"+ bias + GELU, {el:.1f} s"}
-    out["kv_write"] = cpu_kv_write(O, seconds / 4, log)
-    out["attention"] = cpu_attention(seconds / 2, cores, log)
+
+def _cpu_threads(torch, log):
+    """Thread count for the CPU legs: the fastest of os.cpu_count(), the
+    process's CPU affinity and OMP_NUM_THREADS (the GPU box grants each GPU a
+    share of the host's CPUs; threads beyond that share only contend), picked
+    on a short bf16 matmul probe."""
+    cands = {os.cpu_count() or 1, len(os.sched_getaffinity(0))}
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cands.add(int(os.environ["OMP_NUM_THREADS"]))
+    a = torch.randn(128, NS_K).to(torch.bfloat16)
+    b = torch.randn(4096, NS_K).to(torch.bfloat16)
+    probe = {}
+    for n in sorted(cands):
+        torch.set_num_threads(n)
+        probe[n] = _median_seconds(lambda: torch.nn.functional.linear(a, b), reps=3, warmup=1)
+    best = min(probe, key=probe.get)
+    log(f"cpu threads probe (s per 128x3072x4096 bf16 matmul): {probe} -> {best}")
+    return best, {str(k): round(v, 5) for k, v in probe.items()}
+
+
+def cpu_baseline(log):
+    """The reference's own CPU paths for the three kernels, in torch on the
+    host's cores (2 warm-up calls, median of 5 timed ones per leg); each leg
+    times a bounded sample and states how it scales to the full workload."""
+    import torch
+    prev = torch.get_num_threads()
+    cores, probe = _cpu_threads(torch, log)
+    torch.set_num_threads(cores)
+    try:
+        out = cpu_linear(torch, cores, log)
+        out["threads_probe_s"] = probe
+        out["kv_write"] = cpu_kv_write(torch, cores, log)
+        out["attention"] = cpu_attention(torch, cores, log)
+    finally:
+        torch.set_num_threads(prev)
     return out
 
 
-def cpu_kv_write(O, seconds, log):
-    """Config-2 recipe on the host (the reference CPU branch, int8_kv_cache.py:149-158, with
-    448 and the e4m3 cast): the oracle's per-(token, head) quantizer in C, 1 thread, over
-    a 1350-token x 24-head sample of K (1/8 of config 2's K), scaled to config 2's bytes."""
-    import numpy as np
-    rng = np.random.default_rng(1)
-    L = KV_L // 8
-    gain = rng.uniform(0.5, 4.0, KV_H).astype(np.float32)
-    x = O.f32_to_bf16_bits((rng.standard_normal((1, L, KV_H, KV_D)) * gain[None, None, :, None]).astype(np.float32))
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.kv_quantize(x)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
-            break
-    rows = n * L * KV_H
-    gbs = rows * (KV_D * 2 + KV_D + 4) / el / 1e9
-    us_config2 = 2 * KV_L * KV_H * (el / rows) * 1e6
-    log(f"cpu KV write {gbs:.2f} GB/s ({us_config2 / 1e3:.1f} ms for config 2's K and V)")
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "config2_ms_extrapolated": round(us_config2 / 1e3, 2),
-            "sample": f"{n} x [1, {L}, {KV_H}, {KV_D}] bf16 rows through the oracle's KV quantizer (C), {el:.1f} s"}
-
-
-def cpu_attention(seconds, cores, log):
-    """Config-3 reference path on the host (nomas_cpt.py:771-781, attn_mode="torch"): decode
-    the FP8 cache to bf16 with the reference's CPU branch (int8_kv_cache.py:202-204) and run
-    torch's CPU scaled_dot_product_attention, for one head and a 64-query slice over all
-    86 400 keys; TFLOP/s and the time extrapolated to config 3 (x 24 heads x 10800/64)."""
-    import numpy as np
-    import torch
+def cpu_linear(torch, cores, log):
+    """North-star linear through the reference's module path on the CPU
+    (int8_stored_bf16_linear.py:82-94 with e4m3 codes and per-channel scales):
+    dequant_weight() = codes.float() * scale -> bf16, F.linear(x, w, bias) in
+    bf16, then GELU-tanh (nomas_compile_prepost.py:83-84). The weight decode is
+    timed whole (it does not depend on M); the bf16 GEMM on a row sample sized
+    to about a second per call, scaled to M = 10800."""
     import torch.nn.functional as F
-    rng = np.random.default_rng(2)
+    g = torch.Generator().manual_seed(0)
+    codes = (torch.randn(NS_N, NS_K, generator=g) * 0.02 / 1e-4).clamp(-448, 448).to(torch.float8_e4m3fn)
+    scale = torch.full((NS_N, 1), 1e-4)
+    bias = (torch.randn(NS_N, generator=g) * 0.01).to(torch.bfloat16)
+    w = (codes.float() * scale).to(torch.bfloat16)
+
+    def dequant():
+        return (codes.float() * scale).to(torch.bfloat16)
+
+    def gemm(x):
+        return F.gelu(F.linear(x, w, bias), approximate="tanh")
+
+    x64 = torch.randn(64, NS_K, generator=g).to(torch.bfloat16)
+    t64 = _median_seconds(lambda: gemm(x64), reps=1, warmup=1)
+    rows = int(max(64, 64 * 1.0 / max(t64, 1e-6))) // 64 * 64
+    rows = NS_M if rows >= NS_M else rows
+    x = torch.randn(rows, NS_K, generator=g).to(torch.bfloat16)
+    t_dq = _median_seconds(dequant)
+    t_rows = _median_seconds(lambda: gemm(x))
+    t_full = t_dq + t_rows * NS_M / rows
+    tflops = gemm_flops(NS_M, NS_K, NS_N) / t_full / 1e12
+    log(f"cpu linear (torch reference path): dequant {t_dq * 1e3:.1f} ms + {rows}-row bf16 GEMM+GELU "
+        f"{t_rows * 1e3:.1f} ms -> {t_full:.2f} s at M={NS_M}, {tflops * 1e3:.2f} GFLOP/s")
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores,
+            "kind": "reference path (torch CPU)",
+            "north_star_s_extrapolated": round(t_full, 3),
+            "sample": f"dequant_weight of the [{NS_N}, {NS_K}] e4m3 weight (whole, {t_dq * 1e3:.1f} ms) + "
+                      f"bf16 F.linear + bias + GELU-tanh on {rows} of {NS_M} token rows ({t_rows * 1e3:.1f} ms), "
+                      f"median of 5 after 2 warm-ups each; full M = dequant + GEMM x {NS_M}/{rows}"}
+
+
+def cpu_kv_write(torch, cores, log):
+    """Config 2 through the reference's CPU write branch (int8_kv_cache.py:149-158)
+    with the FP8 constants: per (token, head) peak over D, s = peak / 448
+    (1 where the peak is 0), codes = e4m3(x / s); K then V, at full size."""
+    g = torch.Generator().manual_seed(1)
+    gain = torch.empty(KV_H).uniform_(0.5, 4.0, generator=g)
+    k = (torch.randn(1, KV_L, KV_H, KV_D, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+    v = (torch.randn(1, KV_L, KV_H, KV_D, generator=g) * gain[None, None, :, None]).to(torch.bfloat16)
+    q = torch.empty(2, 1, KV_L, KV_H, KV_D, dtype=torch.float8_e4m3fn)
+    sc = torch.empty(2, 1, KV_L, KV_H, 1)
+
+    def write():
+        for i, values in enumerate((k, v)):
+            src = values.float()
+            peak = src.abs().amax(dim=-1, keepdim=True)
+            s = torch.where(peak > 0, peak / 448.0, torch.ones_like(peak))
+            q[i].copy_((src / s).to(torch.float8_e4m3fn))
+            sc[i].copy_(s)
+
+    t = _median_seconds(write)
+    gbs = kv_write_bytes() / t / 1e9
+    log(f"cpu KV write (torch reference branch): {t * 1e3:.1f} ms for config 2, {gbs:.2f} GB/s")
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": cores, "kind": "reference path (torch CPU)",
+            "config2_ms": round(t * 1e3, 2),
+            "sample": f"config 2 whole: K and V [1, {KV_L}, {KV_H}, {KV_D}] bf16 -> e4m3 codes + fp32 scales, "
+                      "median of 5 after 2 warm-ups"}
+
+
+def cpu_attention(torch, cores, log):
+    """Config-3 reference path on the host (nomas_cpt.py:771-781, attn_mode
+    "torch"): decode the FP8 cache to bf16 with the reference's CPU branch
+    (int8_kv_cache.py:202-204), then torch's CPU scaled_dot_product_attention.
+    Sample: the decode of one head's K and V (86 400 keys) and the SDPA of
+    one head's 64-query slice over all keys; config 3 = 24 heads' decode plus
+    24 x 10800/64 such slices."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(2)
     Lk, Lq = ATT_LK, 64
-    codes = torch.from_numpy(rng.integers(0, 0x78, (2, Lk, KV_D), dtype=np.uint8)).view(torch.float8_e4m3fn)
-    scales = torch.from_numpy(rng.uniform(1e-3, 1e-2, (2, Lk, 1)).astype(np.float32))
-    q = torch.randn(1, 1, Lq, KV_D).to(torch.bfloat16)
-    prev = torch.get_num_threads()
-    torch.set_num_threads(cores)
-    try:
-        n, t0 = 0, time.perf_counter()
-        while True:
-            kv = (codes.float() * scales).to(torch.bfloat16)   # the reference's CPU decode
-            k, v = kv[0][None, None], kv[1][None, None]
-            F.scaled_dot_product_attention(q, k, v, scale=KV_D ** -0.5)
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or n >= 50:
-                break
-    finally:
-        torch.set_num_threads(prev)
-    flop = 4.0 * Lq * Lk * KV_D * n
-    tflops = flop / el / 1e12
-    ms3 = el / n * KV_H * (ATT_LQ / Lq) * 1e3
-    log(f"cpu attention {tflops * 1e3:.1f} GFLOP/s ({ms3 / 1e3:.0f} s extrapolated to config 3)")
+    codes = torch.randint(0, 0x78, (2, 1, Lk, 1, KV_D), dtype=torch.uint8, generator=g).view(torch.float8_e4m3fn)
+    scales = torch.empty(2, 1, Lk, 1, 1).uniform_(1e-3, 1e-2, generator=g)
+    q = torch.randn(1, 1, Lq, KV_D, generator=g).to(torch.bfloat16)
+    kv = (codes.float() * scales).to(torch.bfloat16)
+    k, v = kv[0].transpose(1, 2), kv[1].transpose(1, 2)   # [1, 1, Lk, D]
+
+    def decode():
+        return (codes.float() * scales).to(torch.bfloat16)
+
+    t_dec = _median_seconds(decode)
+    t_sdpa = _median_seconds(lambda: F.scaled_dot_product_attention(q, k, v, scale=KV_D ** -0.5))
+    t_full = KV_H * t_dec + KV_H * (ATT_LQ / Lq) * t_sdpa
+    tflops = attn_flops(KV_H, ATT_LQ, Lk, KV_D) / t_full / 1e12
+    log(f"cpu attention (torch reference path): decode {t_dec * 1e3:.1f} ms/head, SDPA {t_sdpa * 1e3:.1f} ms "
+        f"per 64 queries -> {t_full:.0f} s for config 3, {tflops * 1e3:.2f} GFLOP/s")
     return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": cores, "kind": "reference path (torch CPU)",
-            "config3_s_extrapolated": round(ms3 / 1e3, 1),
-            "sample": f"{n} x (decode 2 x {Lk} x {KV_D} FP8 codes + bf16 SDPA of {Lq} queries over "
-                      f"{Lk} keys, one head), {el:.1f} s"}
+            "config3_s_extrapolated": round(t_full, 1),
+            "sample": f"decode of one head's K and V ({Lk} keys, {t_dec * 1e3:.1f} ms) + bf16 SDPA of {Lq} "
+                      f"queries over {Lk} keys ({t_sdpa * 1e3:.1f} ms), median of 5 after 2 warm-ups each; "
+                      f"config 3 = {KV_H} x decode + {KV_H} x {ATT_LQ}/{Lq} x SDPA"}
 
 
 if __name__ == "__main__":
