@@ -16,8 +16,11 @@
 //
 // Per 32-key block the wave computes S^T = K Q^T with
 // v_mfma_f32_32x32x16_bf16: the MFMA output puts one query per lane column,
-// so the online-softmax max is lane-local plus one exchange with lane ^ 32,
-// and the row sum stays lane-local until the end. P^T is packed to fp16 in
+// so a block's max is lane-local. The running max m moves only when a block's
+// logits pass m + 8 (one exchange with lane ^ 32 then makes it the pair's
+// exact max): probabilities stay <= 2^8, and the common path has no
+// cross-lane step. The row sum (of the fp16 probabilities, v_dot2) stays
+// lane-local until the end. P^T is packed to fp16 in
 // registers and is the B operand of O^T += V^T P^T (v_mfma_f32_32x32x16_f16).
 // fp16 probabilities round at 2^-11 relative instead of bf16's 2^-8; V^T is
 // held as the fp16 form of its bf16 value, which is the same number (a bf16
@@ -181,11 +184,13 @@ HN_DEVICE int quad_key(int qd, int j) {
 // Dim group of this thread's V^T quad: lanes 0-31 and 32-63 of a wave take
 // groups whose first rows are 8 apart.
 template <int NW>
-HN_DEVICE int v_group() {
-    const int w = threadIdx.x >> 6, hh = (threadIdx.x & 63) >> 4;
+HN_DEVICE int v_group_of(int tid) {
+    const int w = tid >> 6, hh = (tid & 63) >> 4;
     if constexpr (NW == 4) return 4 * w + hh;                       // 8 dims per group
     else return 4 * w + 2 * (hh & 1) + (hh >> 1);                   // 4 dims per group
 }
+template <int NW>
+HN_DEVICE int v_group() { return v_group_of<NW>(threadIdx.x); }
 
 // Registers holding one cache tile between its global load and its LDS
 // write (issued about one tile ahead).
@@ -318,8 +323,9 @@ HN_DEVICE void k_scales(const float* sb, float (&ks)[Shape<NW>::KU]) {
 // .. + VD/2 - 1 of the thread's VD; keys (0, 1) and (2, 3) pair into dwords
 // of fp16-held bf16 values (vd[2 d + pair], dim d), and parts 6 and 7 write
 // the two halves of the dims (8 bytes = 4 keys each).
+// `vc` holds the thread's codes (as CacheRegs::v), `vt` is the V^T tile.
 template <int FMT, int NW>
-HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const float4& vs,
+HN_DEVICE void store_v_part(const uint32_t (&vc)[4][Shape<NW>::VD / 4], uint8_t* vt, int i, const float4& vs,
                             float (&vp)[Shape<NW>::VD], uint32_t (&vd)[2 * Shape<NW>::VD]) {
     constexpr int VD = Shape<NW>::VD, DP = VD / 2;
     const int j = i >> 1, hf = i & 1;
@@ -328,7 +334,7 @@ HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const fl
 #pragma unroll
     for (int c2 = 0; c2 < DP / 2; ++c2) {
         const int code = DP * hf + 2 * c2;
-        const f32x2 a = codes2_f32<FMT>(r.v[j][code >> 2], (code & 2) != 0);
+        const f32x2 a = codes2_f32<FMT>(vc[j][code >> 2], (code & 2) != 0);
         x[2 * c2] = a[0] * s;
         x[2 * c2 + 1] = a[1] * s;
     }
@@ -343,8 +349,7 @@ HN_DEVICE void store_v_part(const CacheRegs<NW>& r, uint8_t* st, int i, const fl
 #pragma unroll
         for (int dd = 0; dd < DP; ++dd) {
             const int d = DP * hf + dd;
-            *reinterpret_cast<uint2*>(st + K_BYTES + (VD * dg + d) * VTROW + 8 * qd) =
-                make_uint2(vd[2 * d], vd[2 * d + 1]);
+            *reinterpret_cast<uint2*>(vt + (VD * dg + d) * VTROW + 8 * qd) = make_uint2(vd[2 * d], vd[2 * d + 1]);
         }
     }
 }
@@ -368,7 +373,7 @@ HN_DEVICE void store_tile(const CacheRegs<NW>& r, uint8_t* st, const float* sb) 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         store_k_part<FMT, NW>(r, st, i, ks, kd);
-        store_v_part<FMT, NW>(r, st, i, vs, vp, vd);
+        store_v_part<FMT, NW>(r.v, st + K_BYTES, i, vs, vp, vd);
     }
 }
 
@@ -469,37 +474,55 @@ HN_DEVICE f32x16 s_block(const uint8_t* ka, const bf16x8 (&qf)[8]) {
     return acc;
 }
 
-// Max of the raw S^T block over the query's 32 keys (both lanes of the pair).
+// Running state of this lane's query: m, the reference point of the
+// probabilities in log2 units (-inf before any visible key); nm = -m (0 while
+// m = -inf); l, this lane's share of the softmax denominator.
+struct Run {
+    float m, nm, l;
+};
+
+// m may lag the true running max by up to REBASE_SLACK: the probabilities
+// 2^(s c - m) then stay <= 2^REBASE_SLACK, far inside fp16's range, and O, l
+// and m stay consistent (both are relative to m), so the softmax is the same
+// for any such m.
+constexpr float REBASE_SLACK = 8.0f;
+
+// Max of a raw S^T block over this lane's 16 keys of the query (the pair
+// lane holds the other 16; rebase exchanges the two only when it acts).
 HN_DEVICE float raw_max(const f32x16& s) {
     float mx = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
-    return pair_max(mx);
+    return mx;
 }
 
 // Partial tiles: keys j >= lim of the tile, and keys whose bit of the tile's
 // validity word mw is clear, are masked to -inf; returns the new max.
-HN_DEVICE float mask_raw(f32x16& s, int kb, int half, int lim, uint64_t mw) {
+HN_DEVICE float mask_raw(f32x16& u, int kb, int half, int lim, uint64_t mw) {
     const uint32_t bits = (uint32_t)(mw >> (kb * 32 + 4 * half));
+    float mx = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int j = kb * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-        if (j >= lim || !((bits >> (8 * (v >> 2) + (v & 3))) & 1u)) s[v] = -INFINITY;
+        if (j >= lim || !((bits >> (8 * (v >> 2) + (v & 3))) & 1u)) u[v] = -INFINITY;
+        mx = fmaxf(mx, u[v]);
     }
-    return raw_max(s);
+    return mx;
 }
 
-// Running-max update before a block's probabilities: with the block's raw
-// max mx, the logit max in log2 units is mx * c (c = softmax_scale * log2 e
-// > 0). Taken only when some lane's max moved (rare after the first tiles):
-// O and l are rescaled by 2^(m_old - m_new).
-HN_DEVICE void rebase(float mx, float c, float& m, float& l, f32x16 (&o)[4]) {
-    const float mb = mx * c;
-    if (!__any(mb > m)) return;
-    const float mnew = fmaxf(m, mb);
-    const float alpha = m == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
-    m = mnew;
-    l *= alpha;
+// Before a block's probabilities, with the lane's raw block max mx (its
+// logit max in log2 units is mx * c, c = softmax_scale * log2 e > 0): taken,
+// wave-uniformly, only when some lane's logit max passes m + REBASE_SLACK
+// (always when a lane sees its first visible key, m = -inf). Then m moves to
+// the pair's exact max (an LDS-crossbar exchange with lane ^ 32), and O and l
+// are rescaled by 2^(m_old - m_new).
+HN_DEVICE void rebase(float mx, float c, Run& run, f32x16 (&o)[4]) {
+    if (!__any(mx * c > run.m + REBASE_SLACK)) return;
+    const float mnew = fmaxf(run.m, pair_max(mx) * c);
+    const float alpha = run.m == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(run.m - mnew);
+    run.m = mnew;
+    run.nm = mnew == -INFINITY ? 0.0f : -mnew;  // m = -inf: every s is -inf (masked)
+    run.l *= alpha;
     if (__any(alpha != 1.0f)) {
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -515,6 +538,10 @@ HN_DEVICE void rebase(float mx, float c, float& m, float& l, f32x16 (&o)[4]) {
 template <typename A, typename B, typename C>
 HN_DEVICE void pin(A& a, B& b, C& c) {
     asm volatile("" : "+v"(a), "+v"(b), "+v"(c));
+}
+template <typename A, typename B>
+HN_DEVICE void pin(A& a, B& b) {
+    asm volatile("" : "+v"(a), "+v"(b));
 }
 template <typename A>
 HN_DEVICE void pin(A& a) {
@@ -532,18 +559,19 @@ HN_DEVICE void pin(A& a) {
 
 // Step A: S^T of the next block from the K rows at ka (this lane's row in the
 // stage) beside the probabilities of the current block (raw S^T in s):
-// p = 2^(s c - m), l += p, P^T = fp16(p) for the two 16-key slices (registers
-// 8t .. 8t+7 hold keys 16 t + 4 half + {0..3} and + 8 + {0..3} of the block).
-HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, f16x8 (&pf)[2], const uint8_t* ka,
+// p = 2^(s c - m), l += fp16(p), P^T = fp16(p) for the two 16-key slices
+// (registers 8t .. 8t+7 hold keys 16 t + 4 half + {0..3} and + 8 + {0..3} of
+// the block).
+HN_DEVICE f32x16 step_a(const f32x16& s, float c, float nm, float& l, f16x8 (&pf)[2], const uint8_t* ka,
                         const bf16x8 (&qf)[8]) {
-    const float nm = m == -INFINITY ? 0.0f : -m;  // m = -inf: every s is -inf (masked)
     bf16x8 kf[8];
     kf[0] = ld_bf16x8(ka);
     kf[1] = ld_bf16x8(ka + 32);
     f32x16 acc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    float ls[2] = {0.0f, 0.0f};
+    float ls = 0.0f;
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     uint32_t x[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -551,13 +579,13 @@ HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, f16x8 (&pf)
         acc = mfma_bf16(kf[i], qf[i], acc);
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i], c, nm));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * i + 1], c, nm));
-        ls[0] += p0;
-        ls[1] += p1;
         x[i] = pack_f16(p0, p1);
-        pin(x[i], ls[0], ls[1]);
+        // l sums the fp16 probabilities the PV MFMA multiplies (v_dot2_f32_f16)
+        ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x[i]), ones, ls, false);
+        pin(x[i], ls);
         __builtin_amdgcn_sched_barrier(0);
     }
-    l += ls[0] + ls[1];
+    l += ls;
     pf[0] = __builtin_bit_cast(f16x8, make_uint4(x[0], x[1], x[2], x[3]));
     pf[1] = __builtin_bit_cast(f16x8, make_uint4(x[4], x[5], x[6], x[7]));
     return acc;
@@ -566,7 +594,8 @@ HN_DEVICE f32x16 step_a(const f32x16& s, float c, float m, float& l, f16x8 (&pf)
 // Step B: O^T += V^T P^T of block kb (V^T operand reads at va: this lane's
 // row and column in the stage) beside the raw max of the next block (s) and,
 // per STORE (1: K, 2: V^T), half of the write of the prefetched tile to stage
-// nst with the scales of buffer sb. Returns the next block's raw max (pair-wide).
+// nst with the scales of buffer sb. Returns the next block's raw max over this
+// lane's keys.
 template <int FMT, int NW, int STORE>
 HN_DEVICE float step_b(const f16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (&o)[4], const f32x16& s,
                        const CacheRegs<NW>& r, uint8_t* nst, const float* sb) {
@@ -593,10 +622,10 @@ HN_DEVICE float step_b(const f16x8 (&pf)[2], const uint8_t* va, int kb, f32x16 (
         mx = fmaxf(mx, fmaxf(s[2 * i], s[2 * i + 1]));
         pin(mx);
         if (STORE == 1) store_k_part<FMT, NW>(r, nst, i, ks, kd);
-        if (STORE == 2) store_v_part<FMT, NW>(r, nst, i, vs, vp, vd);
+        if (STORE == 2) store_v_part<FMT, NW>(r.v, nst + K_BYTES, i, vs, vp, vd);
         __builtin_amdgcn_sched_barrier(0);
     }
-    return pair_max(mx);
+    return mx;
 }
 
 template <int FMT, int NW, bool MASK>
@@ -666,8 +695,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[i][v] = 0.0f;
-    float m = -INFINITY;  // running max of the logits (log2 units), shared by the lane pair
-    float l = 0.0f;       // this lane's share of the softmax denominator
+    Run run{-INFINITY, 0.0f, 0.0f};  // shared by the lane pair (but l)
     const float c = p.scale_log2;
 
     // Tile t: segment, first key index within it, key count;
@@ -774,8 +802,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 f16x8 pf[2];
 
                 // ---- half 0
-                rebase(mxa, c, m, l, o);
-                sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
+                rebase(mxa, c, run, o);
+                sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
                 // K (and validity word) of tile t + 1 from the prefetch registers
                 // (a tail tile or the end of the range is handled right after:
                 // the stage is not read before the barrier).
@@ -789,8 +817,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
                 const uint64_t mwn = tile_mask<MASK>(nst);
-                rebase(mxb, c, m, l, o);
-                sa = step_a(sb, c, m, l, pf, nst + ka_off, qf);
+                rebase(mxb, c, run, o);
+                sa = step_a(sb, c, run.nm, run.l, pf, nst + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
                 if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
                 if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
@@ -863,8 +891,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 const uint64_t mwn = tile_mask<MASK>(st1);  // tile t + 1 (stale on the last tile)
 
                 // ---- half 0
-                rebase(mxa, c, m, l, o);
-                sb = step_a(sa, c, m, l, pf, st + ka_off + 32 * KROW, qf);
+                rebase(mxa, c, run, o);
+                sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
                 // K (and validity word) of tile t + NS - 1 from the prefetch
                 // registers (a tail tile or the end of the range is handled
                 // right after: the stage is not read before the barrier).
@@ -876,8 +904,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
-                rebase(mxb, c, m, l, o);
-                sa = step_a(sb, c, m, l, pf, st1 + ka_off, qf);
+                rebase(mxb, c, run, o);
+                sa = step_a(sb, c, run.nm, run.l, pf, st1 + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
                 if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
                 if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
@@ -891,7 +919,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             }
         }
     }
-    l += __shfl_xor(l, 32, 64);
+    const float l = run.l + __shfl_xor(run.l, 32, 64);
+    const float m = run.m;
 
     // ---- epilogue: O = O^T / l; the lane holds dims 32 db + 8 (v/4) + 4 half + v%4
     if (p.splits > 1) {
@@ -1054,6 +1083,7 @@ static void launch_kernel(const attn::Params& p, dim3 grid, hipStream_t stream) 
     else
         attn::attn_fp8kv_kernel<HN_KV_INT8, NW, MASK><<<grid, attn::Shape<NW>::NT, 0, stream>>>(p);
 }
+
 
 // One launch of the NW-wave kernel over query rows [row0, row0 + rows) of p's
 // problem (p.Lq = all rows), with `sp` key-range splits merged through the
