@@ -11,9 +11,10 @@ ms / GB/s and the KV-write GB/s ride along in the same JSON line, as does the
 config-1 linear. Timing uses HIP events on the stream the kernels run on.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-seconds S]
-                       [--no-cpu-baseline] [--no-ar] [--only all|linear|kv|attn|copy|ar]
-``--only`` runs one workload (for per-kernel counter passes); ``copy`` is a
-plain 1 GiB device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
+                       [--no-cpu-baseline] [--no-ar] [--only all|linear|kv|attn|decode|copy|ar]
+``--only`` runs one workload (for per-kernel counter passes): ``attn`` config 3,
+``decode`` 128 queries over the same 86 400-key cache; ``copy`` is a plain 1 GiB
+device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
 """
 from __future__ import annotations
 
@@ -101,7 +102,7 @@ def main():
     ap.add_argument("--settle-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
-    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "copy", "ar"])
+    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "decode", "copy", "ar"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -374,16 +375,21 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
         ms = time_loop(lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"],
                                                      cache["v_scale"], k, v, 0), args.steps, args.warmup)
         log(f"KV write {ms * 1e3:.1f} us")
-    elif args.only == "attn":
+    elif args.only in ("attn", "decode"):
         lk = ATT_CHUNKS * KV_L
         cache = kvc.make_fp8_kv_block(1, lk, KV_H, KV_D, device=dev)
         for c in range(ATT_CHUNKS):
             kc = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
             kvc.quantize_kv_pair_into(cache, kc, kc, c * KV_L)
-        q = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
-        ms = time_loop(lambda: ca.chunk_attention(q, cache, lk, q_pos0=lk - KV_L, chunk_len=KV_L),
-                       args.steps, args.warmup)
-        log(f"chunk attention {ms:.3f} ms")
+        if args.only == "attn":
+            q = torch.randn(1, KV_L, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+            ms = time_loop(lambda: ca.chunk_attention(q, cache, lk, q_pos0=lk - KV_L, chunk_len=KV_L),
+                           args.steps, args.warmup)
+            log(f"chunk attention {ms:.3f} ms")
+        else:
+            q = torch.randn(1, 128, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
+            ms = time_loop(lambda: ca.chunk_attention(q, cache, lk), args.steps, args.warmup)
+            log(f"decode-style attention (Lq=128) {ms * 1e3:.1f} us")
 
 
 def gemm_traffic_bytes():

@@ -788,7 +788,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 __syncthreads();
                 mw = tile_mask<MASK>(smem);
                 sa = s_block(smem + ka_off, qf);
-                mxa = g.full && mw == ALL_KEYS ? raw_max(sa) : mask_raw(sa, 0, half, g.lim, mw);
+                mxa = raw_max(sa);
+                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, g.lim, mw);
             }
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
@@ -874,7 +875,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             Geom g = geom(t_begin);
             uint64_t mw = tile_mask<MASK>(smem);  // validity word of tile t
             sa = s_block(smem + ka_off, qf);
-            mxa = g.full && mw == ALL_KEYS ? raw_max(sa) : mask_raw(sa, 0, half, g.lim, mw);
+            mxa = raw_max(sa);
+                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, g.lim, mw);
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
                 const uint8_t* st = smem + (u % NS) * STAGE;              // tile t
