@@ -11,10 +11,12 @@ ms / GB/s and the KV-write GB/s ride along in the same JSON line, as does the
 config-1 linear. Timing uses HIP events on the stream the kernels run on.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-seconds S]
-                       [--no-cpu-baseline] [--no-ar] [--only all|linear|kv|attn|decode|copy|ar]
+                       [--no-cpu-baseline] [--no-ar]
+                       [--only all|linear|kv|attn|decode|blockwise|copy|ar]
 ``--only`` runs one workload (for per-kernel counter passes): ``attn`` config 3,
-``decode`` 128 queries over the same 86 400-key cache; ``copy`` is a plain 1 GiB
-device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
+``decode`` 128 queries over the same 86 400-key cache, ``blockwise`` the decoder
+layer's five blockwise-scaled FP8 GEMMs; ``copy`` is a plain 1 GiB device copy
+used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
 """
 from __future__ import annotations
 
@@ -102,7 +104,8 @@ def main():
     ap.add_argument("--settle-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
-    ap.add_argument("--only", default="all", choices=["all", "linear", "kv", "attn", "decode", "copy", "ar"])
+    ap.add_argument("--only", default="all",
+                    choices=["all", "linear", "kv", "attn", "decode", "blockwise", "copy", "ar"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -178,6 +181,9 @@ def main():
     c1_tflops = gemm_flops(C1_M, C1_K, C1_N) / (ms_c1 * 1e-3) / 1e12
     log(f"config-1 linear {ms_c1 * 1e3:.1f} us ({c1_tflops:.0f} TFLOP/s)")
     del x1, w1
+
+    # ---------------- decoder FP8 linears (blockwise 128x128 scales)
+    dec_res = bench_decoder_linears(args, torch, ops, dev, g, log)
 
     # ---------------- config 2: KV quantize-on-write
     gain = torch.empty(KV_H, device=dev).uniform_(0.5, 4.0, generator=g)
@@ -273,11 +279,46 @@ def main():
                       "decode_lq128_us": round(ms_dec * 1e3, 2),
                       "decode_lq128_gbs": round(dec_gbs, 1),
                       "decode_frac_hbm": round(dec_gbs / HBM_PEAK_GBS, 4)},
+        "decoder_blockwise": dec_res,
         "dit_block": blk_res,
         "ar_chunk": ar_res,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+# The PixelUMM decoder layer's FP8 linears (pixelumm_decoder/model.py:43-53,
+# 203-206,263-265; cutlass_fp8.py:106-121 converts q/o/gate/up/down): hidden
+# 4096, FFN 12288, over one 10800-token window (3 latent frames of 45 x 80).
+DEC_M = 10800
+DEC_LINEARS = (("q_proj", 4096, 4096), ("o_proj", 4096, 4096), ("gate_proj", 4096, 12288),
+               ("up_proj", 4096, 12288), ("down_proj", 12288, 4096))
+
+
+def bench_decoder_linears(args, torch, ops, dev, g, log):
+    """Blockwise-scaled FP8 GEMMs (the reference's gemm(a, b, sa, sb)) at the
+    decoder layer's five FP8 linear shapes, operands quantized once outside
+    the timed loop."""
+    pf = importlib.import_module("hy-nomas_amd.pixelumm_fp8")
+    out, total_ms, total_flop = {}, 0.0, 0.0
+    for name, k, n in DEC_LINEARS:
+        a = torch.randn(DEC_M, k, device=dev, generator=g).to(torch.bfloat16)
+        b = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        qa, sa = pf.quantize_blockwise(a)
+        qb, sb = pf.quantize_blockwise(b)
+        del a, b
+        ms = time_loop(lambda: ops.gemm_fp8_blockwise(qa, qb, sa, sb), args.steps, args.warmup)
+        flop = gemm_flops(DEC_M, k, n)
+        tf = flop / (ms * 1e-3) / 1e12
+        out[name] = {"mkn": [DEC_M, k, n], "us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+        total_ms += ms
+        total_flop += flop
+    tf = total_flop / (total_ms * 1e-3) / 1e12
+    log(f"decoder FP8 linears (blockwise, M={DEC_M}): {total_ms:.3f} ms per layer, {tf:.0f} TFLOP/s; "
+        + ", ".join(f"{k} {v['us']:.0f} us" for k, v in out.items()))
+    out["layer"] = {"ms": round(total_ms, 4), "tflops": round(tf, 1), "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+    return out
 
 
 def block_flops(hidden=3072, heads=24, tokens=KV_L, keys=ATT_CHUNKS * KV_L, d=KV_D, mlp=4):
@@ -375,6 +416,8 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
         ms = time_loop(lambda: ops.kv_quantize_pair_(cache["k"], cache["v"], cache["k_scale"],
                                                      cache["v_scale"], k, v, 0), args.steps, args.warmup)
         log(f"KV write {ms * 1e3:.1f} us")
+    elif args.only == "blockwise":
+        bench_decoder_linears(args, torch, ops, dev, g, log)
     elif args.only in ("attn", "decode"):
         lk = ATT_CHUNKS * KV_L
         cache = kvc.make_fp8_kv_block(1, lk, KV_H, KV_D, device=dev)
