@@ -88,6 +88,8 @@ def assert_close_bf16(got, ref, max_abs=2e-2, rel_l2=1e-2, what="", extra=None, 
     err = float(np.max(diff)) if got.size else 0.0
     denom = float(np.linalg.norm(ref))
     rel = float(np.linalg.norm(got - ref) / denom) if denom > 0 else err
+    if what:
+        print(f"[close] {what}: max-abs {err:.3e} worst/bound {worst:.2f} rel-L2 {rel:.3e}", flush=True)
     assert worst <= 1.0 and rel <= rel_l2, (
         f"{what}: max-abs {err:.3e} (worst/bound {worst:.2f}) rel-L2 {rel:.3e}")
     return err, rel

@@ -381,3 +381,32 @@ def test_attention_reference_invariants(O):
     assert np.allclose(o[0], v2[7], atol=1e-9)
     none = O.attention_reference(q, k, v2, key_valid=np.zeros(Lk, bool))
     assert not none.any()                                                   # no visible key -> zeros
+
+
+def test_strict_bar_needs_the_references_bf16_keys():
+    """Why the attention kernels dequantize K to the reference's values,
+    bf16(code * k_scale), instead of applying the per-key scale to the scores
+    (scores of the unrounded code * k_scale): at config-3 statistics (86 400
+    keys, per-head gain 4) the two softmaxes differ by more than the north
+    star's elementwise bar. float64 throughout; only the K rounding differs."""
+    g = torch.Generator().manual_seed(0)
+    lk, d, nq, gain = 86400, 128, 48, 4.0
+    k = (torch.randn(lk, d, generator=g) * gain).to(torch.bfloat16).double()
+    v = (torch.randn(lk, d, generator=g) * gain).to(torch.bfloat16).double()
+
+    def quant(x):  # the FP8 KV recipe: per-row amax / 448, e4m3 codes
+        s = x.abs().amax(-1, keepdim=True) / 448
+        return (x / s).to(torch.float8_e4m3fn).double(), s
+
+    kc, ks = quant(k)
+    vc, vs = quant(v)
+    k_ref = (kc * ks).to(torch.bfloat16).double()  # int8_kv_cache.py:204 with the e4m3 codes
+    v_ref = (vc * vs).to(torch.bfloat16).double()
+    q = torch.randn(nq, d, generator=g).to(torch.bfloat16).double()
+
+    def attend(kk):
+        return torch.softmax((q @ kk.T) * d ** -0.5, -1) @ v_ref
+
+    o_ref, o_exact_k = attend(k_ref), attend(kc * ks)
+    bound = torch.clamp(1.5 * 2 ** -8 * o_ref.abs(), min=2e-2)
+    assert ((o_exact_k - o_ref).abs() / bound).max() > 1.0
