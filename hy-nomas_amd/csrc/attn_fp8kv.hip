@@ -202,47 +202,75 @@ struct CacheRegs {
     uint32_t mk;                       // MASK: validity of key t - 128 (wave 2)
 };
 
-// Base addresses of a cache tile: uniform (scalar) pointers; the per-thread
-// parts are 32-bit offsets, so the loads take the scalar-base form.
+// A cache tile's loads are buffer loads: per tile one scalar descriptor per
+// array (base = the tile's first key; size = the tile's bytes, so rows past
+// the tile's key count read as zeros -- they are masked out of the softmax --
+// with no per-lane clamp), and per lane a fixed 32-bit offset inside the
+// tile, computed once (LaneOffs).
+constexpr int BUF_FLAGS = 0x00020000;  // raw (stride 0) buffer, 32-bit dwords
+
 struct TileBase {
-    const uint8_t* k;
-    const uint8_t* v;
-    const float* ks;
-    const float* vs;
+    __amdgpu_buffer_rsrc_t k, v, ks, vs;
     const uint8_t* mk;  // validity bytes of the tile's keys, or null (all valid)
 };
 
-HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t first) {
+HN_DEVICE __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUF_FLAGS);
+}
+
+HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t first, int count) {
     TileBase tb;
     const int64_t c = b * p.cs0 + first * p.cs1 + h * p.cs2;
     const int64_t s = b * p.ss0 + first * p.ss1 + h * p.ss2;
-    tb.k = p.kc + c;
-    tb.v = p.vc + c;
-    tb.ks = p.ks + s;
-    tb.vs = p.vs + s;
+    const int64_t cb = (int64_t)(count - 1) * p.cs1 + D;     // codes of keys 0 .. count - 1
+    const int64_t sb = ((int64_t)(count - 1) * p.ss1 + 1) * 4;
+    tb.k = tile_rsrc(p.kc + c, cb);
+    tb.v = tile_rsrc(p.vc + c, cb);
+    tb.ks = tile_rsrc(p.ks + s, sb);
+    tb.vs = tile_rsrc(p.vs + s, sb);
     tb.mk = p.kvalid ? p.kvalid + b * p.kvs + first : nullptr;
     return tb;
 }
 
-// Keys past the end of a short tile re-read the tile's last key (they are
-// masked out of the softmax).
-template <int NW, bool MASK>
-HN_DEVICE void load_k(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int count) {
+// This thread's byte offsets inside a tile: K units (key u / 8, 16 codes at
+// 16 (u % 8)), the VD codes of its V^T quad keys, and its per-key scale
+// (threads < 128: K scales for threads 0-63, V for 64-127).
+template <int NW>
+struct LaneOffs {
+    uint32_t k[Shape<NW>::KU];
+    uint32_t v[4];
+    uint32_t s;
+};
+
+template <int NW>
+HN_DEVICE LaneOffs<NW> lane_offsets(const Params& p) {
+    LaneOffs<NW> o;
     const uint32_t t = threadIdx.x;
-    const uint32_t last = (uint32_t)count - 1u;
 #pragma unroll
-    for (int i = 0; i < Shape<NW>::KU; ++i) {
-        const uint32_t key = min((t >> 3) + (uint32_t)(Shape<NW>::NT / 8) * i, last);
-        r.k[i] = *reinterpret_cast<const uint4*>(tb.k + (key * (uint32_t)p.cs1 + (t & 7u) * 16u));
-    }
+    for (int i = 0; i < Shape<NW>::KU; ++i)
+        o.k[i] = ((t >> 3) + (uint32_t)(Shape<NW>::NT / 8) * i) * (uint32_t)p.cs1 + (t & 7u) * 16u;
+    const int qd = t & 15, dg = v_group<NW>();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.v[j] = (uint32_t)quad_key(qd, j) * (uint32_t)p.cs1 + (uint32_t)(Shape<NW>::VD * dg);
+    o.s = (t & 63u) * (uint32_t)p.ss1 * 4u;
+    return o;
+}
+
+template <int NW, bool MASK>
+HN_DEVICE void load_k(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb, int count) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < Shape<NW>::KU; ++i)
+        r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(tb.k, lo.k[i], 0, 0));
     if (t < 2u * BKV) {
-        const uint32_t so = min(t & 63u, last) * (uint32_t)p.ss1;
-        r.s = t < BKV ? tb.ks[so] : tb.vs[so];
+        // wave-uniform: wave 0 reads K scales, wave 1 V scales
+        const __amdgpu_buffer_rsrc_t sr = t < BKV ? tb.ks : tb.vs;
+        r.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, lo.s, 0, 0));
     }
     if constexpr (MASK) {
         if ((t >> 6) == 2u) {
             const uint32_t j = t & 63u;
-            r.mk = j <= last ? (tb.mk ? (uint32_t)tb.mk[j] : 1u) : 0u;
+            r.mk = (int)j < count ? (tb.mk ? (uint32_t)tb.mk[j] : 1u) : 0u;
         }
     }
 }
@@ -271,20 +299,16 @@ HN_DEVICE uint64_t tile_mask(const uint8_t* st) {
 }
 
 template <int NW>
-HN_DEVICE void load_v(const Params& p, CacheRegs<NW>& r, const TileBase& tb, int count) {
+HN_DEVICE void load_v(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb) {
     constexpr int VD = Shape<NW>::VD;
-    const int qd = threadIdx.x & 15, dg = v_group<NW>();
-    const uint32_t last = (uint32_t)count - 1u;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t key = min((uint32_t)quad_key(qd, j), last);
-        const uint8_t* src = tb.v + (key * (uint32_t)p.cs1 + (uint32_t)(VD * dg));
         if constexpr (VD == 8) {
-            const uint2 x = *reinterpret_cast<const uint2*>(src);
+            const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tb.v, lo.v[j], 0, 0));
             r.v[j][0] = x.x;
             r.v[j][1] = x.y;
         } else {
-            r.v[j][0] = *reinterpret_cast<const uint32_t*>(src);
+            r.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(tb.v, lo.v[j], 0, 0);
         }
     }
 }
@@ -706,7 +730,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
         int64_t first;
         int count;
         bool full;
-        int lim;
+        int64_t pos0;  // position of the tile's key 0
     };
     auto geom = [&](int t) {
         Geom g;
@@ -724,10 +748,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
         }
         g.count = (int)(count < BKV ? count : BKV);
         g.full = g.count == BKV && pos0 + BKV <= wg_key_limit;
-        int64_t lim64 = key_limit - pos0;
-        lim64 = lim64 < g.count ? lim64 : g.count;
-        g.lim = lim64 < 0 ? 0 : (int)lim64;
+        g.pos0 = pos0;
         return g;
+    };
+    // Keys j < lim_of(g) of tile g are visible to this lane's query (taken only
+    // on the masked path).
+    auto lim_of = [&](const Geom& g) {
+        int64_t lim64 = key_limit - g.pos0;
+        lim64 = lim64 < g.count ? lim64 : g.count;
+        return lim64 < 0 ? 0 : (int)lim64;
     };
     // This lane's K row (block 0) at dims 8 half .., and its V^T row (dim
     // block 0) at column unit `half` (slice 0).
@@ -735,6 +764,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     const uint32_t va_off = K_BYTES + col * VTROW + 16 * half;
     CacheRegs<NW> regs;
     regs.s = 0.0f;
+    const LaneOffs<NW> lo = lane_offsets<NW>(p);
 
     // Software pipeline over half tiles. Tile t (u = t - t_begin) is in
     // stage u % NS; during it the wave writes tile t + NS - 1 (dequantized from
@@ -762,9 +792,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             Geom g = geom(t_begin);
             {
                 if (g.cache) {
-                    const TileBase tb = tile_base(p, b, h, g.first);
-                    load_k<NW, MASK>(p, regs, tb, g.count);
-                    load_v<NW>(p, regs, tb, g.count);
+                    const TileBase tb = tile_base(p, b, h, g.first, g.count);
+                    load_k<NW, MASK>(lo, regs, tb, g.count);
+                    load_v<NW>(lo, regs, tb);
                     __builtin_amdgcn_s_waitcnt(0);
                     if (threadIdx.x < 2 * BKV) sbuf[threadIdx.x] = regs.s;
                     __syncthreads();
@@ -776,9 +806,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 if (t_begin + 1 < t_end) {
                     const Geom g1 = geom(t_begin + 1);
                     if (g1.cache) {
-                        const TileBase tb = tile_base(p, b, h, g1.first);
-                        load_k<NW, MASK>(p, regs, tb, g1.count);
-                        load_v<NW>(p, regs, tb, g1.count);
+                        const TileBase tb = tile_base(p, b, h, g1.first, g1.count);
+                        load_k<NW, MASK>(lo, regs, tb, g1.count);
+                        load_v<NW>(lo, regs, tb);
                     }
                 }
                 // Everything issued so far (the Q fragments included) has landed;
@@ -789,7 +819,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 mw = tile_mask<MASK>(smem);
                 sa = s_block(smem + ka_off, qf);
                 mxa = raw_max(sa);
-                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, g.lim, mw);
+                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
             }
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
@@ -810,9 +840,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 // the stage is not read before the barrier).
                 mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
                 store_mask<NW, MASK>(regs, nst);
-                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, g.lim, mw);
+                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, lim_of(g), mw);
                 if (has_next && !gn.cache) copy_tail_k<NW, MASK>(p, b, h, gn.first, gn.count, nst);
-                if (fetch2 && g2.cache) load_k<NW, MASK>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                if (fetch2 && g2.cache) load_k<NW, MASK>(lo, regs, tile_base(p, b, h, g2.first, g2.count), g2.count);
                 __syncthreads();
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
@@ -821,11 +851,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 rebase(mxb, c, run, o);
                 sa = step_a(sb, c, run.nm, run.l, pf, nst + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
-                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
+                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(gn), mwn);
                 if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
                 if (fetch2 && g2.cache) {
                     if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                    load_v<NW>(p, regs, tile_base(p, b, h, g2.first), g2.count);
+                    load_v<NW>(lo, regs, tile_base(p, b, h, g2.first, g2.count));
                 }
                 __syncthreads();
                 g = gn;
@@ -847,9 +877,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 if (t >= t_end) break;
                 const Geom gk = geom(t);
                 if (gk.cache) {
-                    const TileBase tb = tile_base(p, b, h, gk.first);
-                    load_k<NW, MASK>(p, regs, tb, gk.count);
-                    load_v<NW>(p, regs, tb, gk.count);
+                    const TileBase tb = tile_base(p, b, h, gk.first, gk.count);
+                    load_k<NW, MASK>(lo, regs, tb, gk.count);
+                    load_v<NW>(lo, regs, tb);
                     __builtin_amdgcn_s_waitcnt(0);
                     if (threadIdx.x < 2 * BKV) sbuf[(k & 1) * SB_FLOATS + threadIdx.x] = regs.s;
                     __syncthreads();
@@ -862,9 +892,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             if (t_begin + NS - 1 < t_end) {
                 const Geom gk = geom(t_begin + NS - 1);
                 if (gk.cache) {
-                    const TileBase tb = tile_base(p, b, h, gk.first);
-                    load_k<NW, MASK>(p, regs, tb, gk.count);
-                    load_v<NW>(p, regs, tb, gk.count);
+                    const TileBase tb = tile_base(p, b, h, gk.first, gk.count);
+                    load_k<NW, MASK>(lo, regs, tb, gk.count);
+                    load_v<NW>(lo, regs, tb);
                 }
             }
             // Everything issued so far (the Q fragments included) has landed;
@@ -876,7 +906,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             uint64_t mw = tile_mask<MASK>(smem);  // validity word of tile t
             sa = s_block(smem + ka_off, qf);
             mxa = raw_max(sa);
-                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, g.lim, mw);
+                if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
             for (int t = t_begin; t < t_end; ++t) {
                 const int u = t - t_begin;
                 const uint8_t* st = smem + (u % NS) * STAGE;              // tile t
@@ -900,20 +930,20 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 // right after: the stage is not read before the barrier).
                 mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
                 store_mask<NW, MASK>(regs, wst);
-                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, g.lim, mw);
+                if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, lim_of(g), mw);
                 if (write && !gw.cache) copy_tail_k<NW, MASK>(p, b, h, gw.first, gw.count, wst);
-                if (fetch && gf.cache) load_k<NW, MASK>(p, regs, tile_base(p, b, h, gf.first), gf.count);
+                if (fetch && gf.cache) load_k<NW, MASK>(lo, regs, tile_base(p, b, h, gf.first, gf.count), gf.count);
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
                 rebase(mxb, c, run, o);
                 sa = step_a(sb, c, run.nm, run.l, pf, st1 + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
-                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, gn.lim, mwn);
+                if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(gn), mwn);
                 if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
                 if (fetch && gf.cache) {
                     if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                    load_v<NW>(p, regs, tile_base(p, b, h, gf.first), gf.count);
+                    load_v<NW>(lo, regs, tile_base(p, b, h, gf.first, gf.count));
                 }
                 __syncthreads();
                 g = gn;
