@@ -218,12 +218,15 @@ HN_DEVICE __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUF_FLAGS);
 }
 
+// count = 0 gives empty descriptors: every load through them reads zeros and
+// touches no memory (the loop issues its prefetch loads unconditionally, so
+// that their order, and with it every wait on them, is the same on all paths).
 HN_DEVICE TileBase tile_base(const Params& p, int64_t b, int64_t h, int64_t first, int count) {
     TileBase tb;
     const int64_t c = b * p.cs0 + first * p.cs1 + h * p.cs2;
     const int64_t s = b * p.ss0 + first * p.ss1 + h * p.ss2;
-    const int64_t cb = (int64_t)(count - 1) * p.cs1 + D;     // codes of keys 0 .. count - 1
-    const int64_t sb = ((int64_t)(count - 1) * p.ss1 + 1) * 4;
+    const int64_t cb = count > 0 ? (int64_t)(count - 1) * p.cs1 + D : 0;  // codes of keys 0 .. count - 1
+    const int64_t sb = count > 0 ? ((int64_t)(count - 1) * p.ss1 + 1) * 4 : 0;
     tb.k = tile_rsrc(p.kc + c, cb);
     tb.v = tile_rsrc(p.vc + c, cb);
     tb.ks = tile_rsrc(p.ks + s, sb);
@@ -256,17 +259,26 @@ HN_DEVICE LaneOffs<NW> lane_offsets(const Params& p) {
     return o;
 }
 
+// `co` / `so`: a tile's byte offset inside descriptors that start before it
+// (the steady loop's span descriptors), added to every lane's code / scale
+// offset; 0 with per-tile descriptors.
 template <int NW, bool MASK>
-HN_DEVICE void load_k(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb, int count) {
+HN_DEVICE void load_k(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb, int count, uint32_t co = 0,
+                      uint32_t so = 0) {
     const uint32_t t = threadIdx.x;
+    // Wave 0 reads the K scales, wave 1 the V scales. The wave index goes
+    // through readfirstlane so that the descriptor choice is a scalar one (a
+    // per-lane choice of descriptor would be a loop over its distinct values).
+    // The scale load is issued before the codes: its consumer (the scale
+    // buffer write) then waits for it alone.
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    if (wv < 2u) {
+        const __amdgpu_buffer_rsrc_t sr = wv == 0u ? tb.ks : tb.vs;
+        r.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, lo.s + so, 0, 0));
+    }
 #pragma unroll
     for (int i = 0; i < Shape<NW>::KU; ++i)
-        r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(tb.k, lo.k[i], 0, 0));
-    if (t < 2u * BKV) {
-        // wave-uniform: wave 0 reads K scales, wave 1 V scales
-        const __amdgpu_buffer_rsrc_t sr = t < BKV ? tb.ks : tb.vs;
-        r.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, lo.s, 0, 0));
-    }
+        r.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(tb.k, lo.k[i] + co, 0, 0));
     if constexpr (MASK) {
         if ((t >> 6) == 2u) {
             const uint32_t j = t & 63u;
@@ -299,16 +311,16 @@ HN_DEVICE uint64_t tile_mask(const uint8_t* st) {
 }
 
 template <int NW>
-HN_DEVICE void load_v(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb) {
+HN_DEVICE void load_v(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb, uint32_t co = 0) {
     constexpr int VD = Shape<NW>::VD;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         if constexpr (VD == 8) {
-            const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tb.v, lo.v[j], 0, 0));
+            const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(tb.v, lo.v[j] + co, 0, 0));
             r.v[j][0] = x.x;
             r.v[j][1] = x.y;
         } else {
-            r.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(tb.v, lo.v[j], 0, 0);
+            r.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(tb.v, lo.v[j] + co, 0, 0);
         }
     }
 }
@@ -766,6 +778,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     regs.s = 0.0f;
     const LaneOffs<NW> lo = lane_offsets<NW>(p);
 
+    // Steady tiles: the prefix [t_begin, t_fast) of the range in which the
+    // current and the next tile are full cache tiles (every key exists and is
+    // visible to every query: nothing to mask) and the tiles written and
+    // fetched are cache tiles -- the bulk of any long range. They run a loop
+    // with no per-tile geometry, tail or mask branches, loading through
+    // descriptors that span the (b, h) cache rows [0, cache_end) at the
+    // tile's byte offset (so the span must fit 31 bits). Kernels with
+    // validity masks take the general loop throughout.
+    const int64_t full_end = cache_end < wg_key_limit ? cache_end : wg_key_limit;
+    const int n_full = full_end > 0 ? (int)(full_end / BKV) : 0;
+    const bool span_ok = !MASK && cache_end > 0 && p.cs1 > 0 && p.ss1 > 0 &&
+                         (cache_end - 1) * p.cs1 + D < ((int64_t)1 << 31) &&
+                         ((cache_end - 1) * p.ss1 + 1) * 4 < ((int64_t)1 << 31);
+    int t_fast = t_begin;
+    if (span_ok) {
+        int tf = n_full - 1;
+        tf = tf < t_end - NS ? tf : t_end - NS;
+        tf = tf < n_cache - NS ? tf : n_cache - NS;
+        t_fast = tf > t_begin ? tf : t_begin;
+    }
+    const TileBase span = tile_base(p, b, h, 0, span_ok ? (int)cache_end : 0);
+    const uint32_t tile_co = (uint32_t)(BKV * p.cs1), tile_so = (uint32_t)(BKV * p.ss1 * 4);
+
     // Software pipeline over half tiles. Tile t (u = t - t_begin) is in
     // stage u % NS; during it the wave writes tile t + NS - 1 (dequantized from
     // the prefetch registers, scales from buffer (u + NS - 1) % 2) to stage
@@ -821,7 +856,34 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 mxa = raw_max(sa);
                 if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
             }
-            for (int t = t_begin; t < t_end; ++t) {
+            int t = t_begin;
+            if constexpr (!MASK) {
+                // steady tiles (see t_fast): fetch tile t + 2 at offsets fco / fso
+                uint32_t fco = (uint32_t)((int64_t)(t + 2) * BKV * p.cs1);
+                uint32_t fso = (uint32_t)((int64_t)(t + 2) * BKV * p.ss1 * 4);
+                for (; t < t_fast; ++t) {
+                    const int u = t - t_begin;
+                    const uint8_t* st = smem + (u & 1) * STAGE;
+                    uint8_t* nst = smem + ((u & 1) ^ 1) * STAGE;
+                    const float* nsb = sbuf + ((u & 1) ^ 1) * SB_FLOATS;
+                    f16x8 pf[2];
+                    rebase(mxa, c, run, o);
+                    sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
+                    mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
+                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso);
+                    __syncthreads();
+                    rebase(mxb, c, run, o);
+                    sa = step_a(sb, c, run.nm, run.l, pf, nst + ka_off, qf);
+                    mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
+                    if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                    load_v<NW>(lo, regs, span, fco);
+                    __syncthreads();
+                    fco += tile_co;
+                    fso += tile_so;
+                }
+                if (t > t_begin) g = geom(t);
+            }
+            for (; t < t_end; ++t) {
                 const int u = t - t_begin;
                 const uint8_t* st = smem + (u & 1) * STAGE;
                 uint8_t* nst = smem + ((u & 1) ^ 1) * STAGE;
@@ -842,7 +904,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 store_mask<NW, MASK>(regs, nst);
                 if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, lim_of(g), mw);
                 if (has_next && !gn.cache) copy_tail_k<NW, MASK>(p, b, h, gn.first, gn.count, nst);
-                if (fetch2 && g2.cache) load_k<NW, MASK>(lo, regs, tile_base(p, b, h, g2.first, g2.count), g2.count);
+                const int n2 = fetch2 && g2.cache ? g2.count : 0;  // 0: no fetch (zeros)
+                load_k<NW, MASK>(lo, regs, tile_base(p, b, h, g2.first, n2), n2);
                 __syncthreads();
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
@@ -853,10 +916,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
                 if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(gn), mwn);
                 if (has_next && !gn.cache) copy_tail_v<NW>(p, b, h, gn.first, gn.count, nst);
-                if (fetch2 && g2.cache) {
-                    if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                    load_v<NW>(lo, regs, tile_base(p, b, h, g2.first, g2.count));
-                }
+                // (without a fetch: zeros into a scale buffer no write reads)
+                if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                load_v<NW>(lo, regs, tile_base(p, b, h, g2.first, n2));
                 __syncthreads();
                 g = gn;
                 mw = mwn;
@@ -907,7 +969,38 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             sa = s_block(smem + ka_off, qf);
             mxa = raw_max(sa);
                 if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
-            for (int t = t_begin; t < t_end; ++t) {
+            int t = t_begin;
+            if constexpr (!MASK) {
+                // steady tiles (see t_fast): fetch tile t + NS at offsets fco / fso
+                uint32_t fco = (uint32_t)((int64_t)(t + NS) * BKV * p.cs1);
+                uint32_t fso = (uint32_t)((int64_t)(t + NS) * BKV * p.ss1 * 4);
+                int s0 = 0;  // stage of tile t, (t - t_begin) % NS
+                for (; t < t_fast; ++t) {
+                    const int u = t - t_begin;
+                    const int s1 = s0 == NS - 1 ? 0 : s0 + 1;  // tile t + 1
+                    const int sw = s0 == 0 ? NS - 1 : s0 - 1;  // tile t + NS - 1
+                    const uint8_t* st = smem + s0 * STAGE;
+                    const uint8_t* st1 = smem + s1 * STAGE;
+                    uint8_t* wst = smem + sw * STAGE;
+                    const float* wsb = sbuf + ((u + NS - 1) & 1) * SB_FLOATS;
+                    f16x8 pf[2];
+                    rebase(mxa, c, run, o);
+                    sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
+                    mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
+                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso);
+                    rebase(mxb, c, run, o);
+                    sa = step_a(sb, c, run.nm, run.l, pf, st1 + ka_off, qf);
+                    mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
+                    if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                    load_v<NW>(lo, regs, span, fco);
+                    __syncthreads();
+                    fco += tile_co;
+                    fso += tile_so;
+                    s0 = s1;
+                }
+                if (t > t_begin) g = geom(t);
+            }
+            for (; t < t_end; ++t) {
                 const int u = t - t_begin;
                 const uint8_t* st = smem + (u % NS) * STAGE;              // tile t
                 const uint8_t* st1 = smem + ((u + 1) % NS) * STAGE;       // tile t + 1
@@ -932,7 +1025,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 store_mask<NW, MASK>(regs, wst);
                 if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, lim_of(g), mw);
                 if (write && !gw.cache) copy_tail_k<NW, MASK>(p, b, h, gw.first, gw.count, wst);
-                if (fetch && gf.cache) load_k<NW, MASK>(lo, regs, tile_base(p, b, h, gf.first, gf.count), gf.count);
+                const int nf = fetch && gf.cache ? gf.count : 0;  // 0: no fetch (zeros)
+                load_k<NW, MASK>(lo, regs, tile_base(p, b, h, gf.first, nf), nf);
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
@@ -941,10 +1035,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
                 if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(gn), mwn);
                 if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
-                if (fetch && gf.cache) {
-                    if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
-                    load_v<NW>(lo, regs, tile_base(p, b, h, gf.first, gf.count));
-                }
+                // (without a fetch: zeros into a scale buffer no write reads)
+                if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
+                load_v<NW>(lo, regs, tile_base(p, b, h, gf.first, nf));
                 __syncthreads();
                 g = gn;
                 mw = mwn;
