@@ -1,0 +1,179 @@
+// Issue-rate microbenchmark for gfx950: what one SIMD sustains when a wave's
+// instruction stream mixes v_mfma_f32_32x32x16_bf16 with VALU work, and what
+// the chunk attention's per-tile slot mix allows at most.
+//
+// Every kernel runs 256 workgroups (one per CU; the 96 KB of LDS each takes
+// keeps a second one off the CU) of 256, 512 or 768 threads, i.e. 1, 2 or 3
+// waves per SIMD, for a fixed number of "slots". A slot is one MFMA (or none)
+// followed by the VALU instructions of its pattern, fenced with
+// sched_barrier so the compiler keeps that order. Reported per SIMD: wall
+// nanoseconds per slot (hipEvent timing of the whole launch) and the MFMA
+// share of that time against the MFMA-only launch at the same occupancy.
+//
+// Patterns:
+//   mfma            1 MFMA per slot (dependent accumulator chain)
+//   valu N          N v_fma_f32 per slot, no MFMA
+//   mfma+N          1 MFMA + N v_fma_f32 in the same wave
+//   split N         even waves MFMA only, odd waves N v_fma_f32 only
+//   tile            the attention's tile: 16 step-A slots (MFMA + 2 fma,
+//                   2 exp, 1 cvt_pk_f16, 1 dot2), 8 K-write slots (MFMA +
+//                   fp8 cvt, 2 mul, cvt_pk_bf16, max3), 8 V-write slots (the
+//                   same + 2 unpack + cvt_pkrtz); each MFMA's A operand read
+//                   from LDS two slots ahead, as the kernel does.
+//
+// Build: hy-nomas_amd/build.py (build_probes) -> hy-nomas_amd/probes/issue_rates
+// Run:   hy-nomas_amd/probes/issue_rates   (one GPU, about a second)
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+#define CHECK(x)                                                                       \
+    do {                                                                               \
+        hipError_t e_ = (x);                                                           \
+        if (e_ != hipSuccess) {                                                        \
+            fprintf(stderr, "%s: %s\n", #x, hipGetErrorString(e_));                    \
+            exit(1);                                                                   \
+        }                                                                              \
+    } while (0)
+
+constexpr int SLOTS = 32;  // slots per loop iteration (one attention tile per wave)
+constexpr int LDS_BYTES = 96 * 1024;
+
+enum Pattern { MFMA = 0, VALU = 1, MFMA_VALU = 2, SPLIT = 3, TILE = 4 };
+
+__device__ __forceinline__ void fma_op(float& x, float c) { asm volatile("v_fma_f32 %0, %0, %1, 0.5" : "+v"(x) : "v"(c)); }
+
+// The VALU work of one attention slot of kind k (0: step A, 1: K write, 2: V write).
+__device__ __forceinline__ void tile_valu(int k, float (&x)[12], float c, uint32_t w) {
+    if (k == 0) {
+        asm volatile("v_fma_f32 %0, %0, %1, %2" : "+v"(x[0]) : "v"(c), "v"(x[8]));
+        asm volatile("v_fma_f32 %0, %0, %1, %2" : "+v"(x[1]) : "v"(c), "v"(x[8]));
+        asm volatile("v_exp_f32 %0, %0" : "+v"(x[0]));
+        asm volatile("v_exp_f32 %0, %0" : "+v"(x[1]));
+        asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(x[2]) : "v"(x[0]), "v"(x[1]));
+        asm volatile("v_dot2c_f32_f16 %0, %1, %2" : "+v"(x[3]) : "v"(x[2]), "v"(x[9]));
+    } else {
+        asm volatile("v_cvt_scalef32_pk_f32_fp8 %0, %1, 1.0" : "=v"(*reinterpret_cast<double*>(&x[4])) : "v"(w));
+        asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x[4]) : "v"(c));
+        asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x[5]) : "v"(c));
+        asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(x[6]) : "v"(x[4]), "v"(x[5]));
+        if (k == 2) {
+            asm volatile("v_lshlrev_b32 %0, 16, %1" : "=v"(x[2]) : "v"(x[6]));
+            asm volatile("v_and_b32 %0, 0xffff0000, %1" : "=v"(x[3]) : "v"(x[6]));
+            asm volatile("v_cvt_pkrtz_f16_f32 %0, %1, %2" : "=v"(x[9]) : "v"(x[2]), "v"(x[3]));
+        }
+        asm volatile("v_max3_f32 %0, %0, %1, %2" : "+v"(x[7]) : "v"(x[10]), "v"(x[11]));
+    }
+}
+
+// The slot loop of one wave role (compile-time: MFMA issued, VALU pattern).
+// VK: 0 none, 1 NV x v_fma_f32, 2 the attention slot mix (with LDS operands).
+template <bool MF, int VK, int NV>
+__device__ float slot_loop(int iters, const uint8_t* lds) {
+    f32x16 acc[2];
+    for (int a = 0; a < 2; ++a)
+        for (int v = 0; v < 16; ++v) acc[a][v] = 0.0f;
+    bf16x8 qa, qb;
+    for (int i = 0; i < 8; ++i) {
+        qa[i] = (__bf16)(0.001f * (threadIdx.x + i));
+        qb[i] = (__bf16)(0.002f * i);
+    }
+    float x[12];
+    for (int i = 0; i < 12; ++i) x[i] = 0.01f * (threadIdx.x + i);
+    const float c = 0.999f;
+    const uint32_t w = 0x38383838u + threadIdx.x;
+    const uint8_t* base = lds + (threadIdx.x & 63) * 272;
+    for (int it = 0; it < iters; ++it) {
+        bf16x8 f[SLOTS];
+        if (VK == 2) {
+            f[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base));
+            f[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + 32));
+        }
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            if (VK == 2 && s + 2 < SLOTS)
+                f[s + 2] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(base + 32 * ((s + 2) & 7) + 4096 * ((s + 2) >> 3)));
+            if (MF) acc[s & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(VK == 2 ? f[s] : qa, qb, acc[s & 1], 0, 0, 0);
+            if (VK == 1) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j) fma_op(x[j % 12], c);
+            }
+            if (VK == 2) tile_valu(s < 16 ? 0 : s < 24 ? 1 : 2, x, c, w);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float sum = 0.0f;
+    for (int a = 0; a < 2; ++a)
+        for (int v = 0; v < 16; ++v) sum += acc[a][v];
+    for (int i = 0; i < 12; ++i) sum += x[i];
+    return sum;
+}
+
+template <int PAT, int NV>
+__global__ void issue_kernel(int iters, float* out) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+    for (int i = threadIdx.x; i < LDS_BYTES / 4; i += blockDim.x) reinterpret_cast<uint32_t*>(lds)[i] = 0x3c003c00u ^ i;
+    __syncthreads();
+    float sum;
+    if (PAT == MFMA) sum = slot_loop<true, 0, 0>(iters, lds);
+    else if (PAT == VALU) sum = slot_loop<false, 1, NV>(iters, lds);
+    else if (PAT == MFMA_VALU) sum = slot_loop<true, 1, NV>(iters, lds);
+    else if (PAT == TILE) sum = slot_loop<true, 2, 0>(iters, lds);
+    else if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 1) sum = slot_loop<false, 1, NV>(iters, lds);
+    else sum = slot_loop<true, 0, 0>(iters, lds);  // SPLIT: even waves MFMA, odd waves VALU
+    out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
+}
+
+template <int PAT, int NV>
+double run(int threads, float* out) {
+    const int blocks = 256, iters = 1000;
+    hipLaunchKernelGGL((issue_kernel<PAT, NV>), dim3(blocks), dim3(threads), 0, 0, 1, out);
+    CHECK(hipGetLastError());
+    CHECK(hipDeviceSynchronize());
+    hipEvent_t e0, e1;
+    CHECK(hipEventCreate(&e0));
+    CHECK(hipEventCreate(&e1));
+    CHECK(hipEventRecord(e0, 0));
+    hipLaunchKernelGGL((issue_kernel<PAT, NV>), dim3(blocks), dim3(threads), 0, 0, iters, out);
+    CHECK(hipGetLastError());
+    CHECK(hipEventRecord(e1, 0));
+    CHECK(hipEventSynchronize(e1));
+    float ms = 0.0f;
+    CHECK(hipEventElapsedTime(&ms, e0, e1));
+    CHECK(hipEventDestroy(e0));
+    CHECK(hipEventDestroy(e1));
+    // per SIMD slot: every wave of the SIMD runs SLOTS * iters slots
+    return ms * 1e6 / (double(SLOTS) * iters * (threads / 256));
+}
+
+int main() {
+    float* out = nullptr;
+    CHECK(hipMalloc(&out, 256 * 768 * sizeof(float)));
+    printf("%-40s %6s %12s %10s\n", "pattern", "w/SIMD", "ns/slot", "MFMA share");
+    for (int threads : {256, 512, 768}) {
+        const int wps = threads / 256;
+        const double base = run<MFMA, 0>(threads, out);
+        // MFMA share: the MFMA-only launch's time per MFMA over this pattern's
+        // (frac: share of the waves that issue MFMAs)
+        auto line = [&](const char* name, double ns, bool has_mfma, double frac = 1.0) {
+            if (has_mfma)
+                printf("%-40s %6d %12.2f %9.1f%%\n", name, wps, ns, 100.0 * base * frac / ns);
+            else
+                printf("%-40s %6d %12.2f %10s\n", name, wps, ns, "-");
+        };
+        line("mfma", base, true);
+        line("valu 8", run<VALU, 8>(threads, out), false);
+        line("mfma+4", run<MFMA_VALU, 4>(threads, out), true);
+        line("mfma+8", run<MFMA_VALU, 8>(threads, out), true);
+        if (wps > 1) line("split 8 (even: mfma, odd: 8 valu)", run<SPLIT, 8>(threads, out), true, 0.5);
+        line("tile (attention slot mix + LDS reads)", run<TILE, 0>(threads, out), true);
+    }
+    CHECK(hipFree(out));
+    return 0;
+}
