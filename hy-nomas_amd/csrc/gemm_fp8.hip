@@ -4,21 +4,20 @@
 //   out[m, n] = epilogue( sum_k a[m, k] * b[n, k] )
 //
 // a: activations [M, K] and b: weights [N, K], both K-contiguous e4m3 (the
-// nn.Linear weight layout). Two scale modes share one mainloop:
+// nn.Linear weight layout). Two scale modes:
 //   ROWCOL    per-token x per-output-channel scales, bias and optional
-//             GELU-tanh fused in the epilogue;
+//             GELU-tanh fused in the epilogue (gemm_rowcol_oe_kernel, a
+//             persistent 4-wave kernel; gemm_rowcol_kernel for short K);
 //   BLOCKWISE 128x128 block scales on both operands (the decoder contract):
-//             each 128-wide K step is promoted into the accumulator with its
-//             own sa * sb factor.
+//             each 128-wide K step is promoted with its own sa * sb factor
+//             (gemm_bw8_kernel, 8 waves).
 //
-// Tiling: a 256-thread workgroup (4 waves, 2 x 2) owns a 256 x 256 output
-// tile; each wave owns 128 x 128 = 4 x 4 MFMA blocks of 32 x 32 (256 fp32
-// accumulators per lane). K advances 128 bytes per step through two LDS
-// stages (2 x 64 KB of the 160 KB per CU): while the MFMAs consume stage s,
-// the next K step's global loads are in flight and land in stage s^1.
-// Rows are 128 bytes in LDS with their eight 16-byte chunks XOR-swizzled by
-// (row & 7), so the 16-byte fragment reads of eight consecutive rows hit
-// eight distinct bank groups.
+// Tiling: a workgroup owns a 256 x 256 output tile; with 4 waves (2 x 2) each
+// wave owns 128 x 128 = 4 x 4 MFMA blocks of 32 x 32 (256 fp32 accumulators
+// per lane), with 8 waves (2 x 4) 128 x 64. K advances 128 bytes per step
+// through LDS buffers filled by direct global -> LDS loads. Rows are 128
+// bytes in LDS with their eight 16-byte chunks XOR-swizzled (swz_pos), so the
+// 16-byte fragment reads of consecutive rows hit distinct bank groups.
 //
 // The MFMA's first operand is the weight tile and its second the activation
 // tile, i.e. the wave computes out^T: each lane then holds four consecutive
@@ -98,21 +97,6 @@ HN_DEVICE void dma_16B(const uint8_t* gsrc, uint32_t lds_addr) {
 
 HN_DEVICE uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-HN_DEVICE void load_tile_lds(uint8_t* lds_tile, const uint8_t* __restrict__ base, int64_t row0,
-                             int64_t rows, int64_t K, int64_t k0, int wave, int lane) {
-    const uint32_t tile_addr = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int rgn = wave * 8 + i;
-        const int r = rgn * 8 + (lane >> 3);
-        const int c = swz_pos(r, lane & 7);  // the swizzle is an involution
-        int64_t row = row0 + r;
-        row = row < rows ? row : rows - 1;
-        dma_16B(base + row * K + k0 + (c << 4),
-                __builtin_amdgcn_readfirstlane(tile_addr + rgn * 1024));
-    }
 }
 
 // One 32 x 64 fragment: lane l reads row (l % 32) of the block and the 32
@@ -257,19 +241,68 @@ HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_
         epilogue_act<MODE, HN_ACT_NONE>(acc, p, m0, n0, smem, wave, wm, wn, lane, imax, jmax);
 }
 
-template <int MODE>
-__global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
-    // BLOCKWISE: the wave pair's scale rows, staged once so the K loop needs
-    // no global scale loads: [2 m blocks][KT] then [2 n blocks][KT].
+// ---------------------------------------------------------------------------
+// Blockwise-scaled kernel, 8 waves: a 512-thread workgroup owns a 256 x 256
+// output tile; wave w owns rows 128 (w % 2) .. + 127 and columns 64 (w / 2)
+// .. + 63, i.e. 4 x 2 MFMA blocks of 32 x 32 (128 fp32 accumulators per
+// lane, held in VGPRs), two waves per SIMD. K advances 128 bytes per step
+// through two LDS stages (A and B tiles, 2 x 64 KB): while the MFMAs consume
+// stage s, the next step's loads land in stage s ^ 1.
+//
+// Scale promotion without a second accumulator set: the wave's sub-tile lies
+// inside one 128 x 128 scale block of each operand, so K block kt has one
+// factor f_kt = sa[mb][kt] * sb[nb][kt] for the whole sub-tile. The
+// accumulators are kept in units of the current block's factor:
+//     acc_kt = acc_(kt-1) * (f_(kt-1) / f_kt) + A_kt B_kt^T,  out = acc * f_last,
+// which is sum_kt f_kt A_kt B_kt^T up to fp32 rounding of the rescale (one
+// multiply per accumulator per K block, ~2^-24 relative each). A block with
+// f_kt = 0 contributes nothing and is skipped, so f is never divided by 0.
+// The rescale of an MFMA block is issued right before that block's first
+// MFMA of the step, so it runs beside the previous block's MFMA.
+constexpr int NT8 = 512;
+
+// Direct global -> LDS loads of one 256 x 128 operand tile by 8 waves: wave w
+// fills the 1 KB regions 4 w .. 4 w + 3 (rows 32 w .. 32 w + 31), lane l at
+// row l / 8 of its region, physical chunk l % 8 (the logical chunk the
+// swizzle puts there). Rows past the operand's end are clamped to its last
+// row: in bounds, never stored.
+HN_DEVICE void load_tile_lds8(uint8_t* lds_tile, const uint8_t* __restrict__ base, int64_t row0, int64_t rows,
+                              int64_t K, int64_t k0, int wave, int lane) {
+    const uint32_t tile_addr = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rgn = wave * 4 + i;
+        const int r = rgn * 8 + (lane >> 3);
+        const int c = swz_pos(r, lane & 7);  // the swizzle is an involution
+        int64_t row = row0 + r;
+        row = row < rows ? row : rows - 1;
+        dma_16B(base + row * K + k0 + (c << 4), __builtin_amdgcn_readfirstlane(tile_addr + rgn * 1024));
+    }
+}
+
+// The fragments of one 64-byte K slice for the wave's 128 x 64 sub-tile.
+struct Frags8 {
+    i32x8 b[2];
+    i32x8 a[4];
+};
+
+HN_DEVICE void read_slice8(Frags8& f, const uint8_t* a_buf, const uint8_t* b_buf, int kh, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) f.b[i] = read_frag(b_buf, wn * 64 + i * 32 + (lane & 31), kh, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.a[j] = read_frag(a_buf, wm * 128 + j * 32 + (lane & 31), kh, lane);
+}
+
+__global__ __launch_bounds__(NT8, 1) void gemm_bw8_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE_BYTES];
+    // the tile's scale rows: [2 m blocks][KT] then [2 n blocks][KT]
     __shared__ float sscale[4 * kMaxKT];
 
     // Tile order. Workgroup ids are dealt round-robin to the 8 XCDs, each with
     // its own L2, so id % 8 selects a contiguous range of work items for that
     // XCD. Work items are laid out in groups of GROUP_M tile rows, walking N
-    // inside a group: the ~32 tiles an XCD runs at once then cover GROUP_M
-    // activation tiles x 32/GROUP_M weight tiles, each fetched once into that
-    // L2 and reused by the other workgroups.
+    // inside a group: the tiles an XCD runs at once then share their A and B
+    // panels in that L2.
     const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
     if (w >= p.tiles_m * p.tiles_n) return;
     const int per_group = GROUP_M * p.tiles_n;
@@ -280,78 +313,97 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(Params p) {
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave & 1, wn = wave >> 1;  // wave's 128 x 128 sub-tile
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1;  // rows 128 wm .., columns 64 wn ..
     const int KT = (int)(p.K / BK);
 
-    if (MODE == BLOCKWISE) {
-        // Blocks wholly past M or N get zero: they are computed, never stored.
-        for (int i = threadIdx.x; i < 4 * KT; i += NT) {
-            const int which = i / KT, kb = i % KT;
-            float v = 0.0f;
-            if (which < 2) {
-                const int64_t mb = (m0 >> 7) + which;
-                if (mb * 128 < p.M) v = p.sa[mb * KT + kb];
-            } else {
-                const int64_t nb = (n0 >> 7) + (which - 2);
-                if (nb * 128 < p.N) v = p.sb[nb * KT + kb];
-            }
-            sscale[i] = v;
+    // Blocks wholly past M or N get factor 0: skipped, never stored.
+    for (int i = threadIdx.x; i < 4 * KT; i += NT8) {
+        const int which = i / KT, kb = i % KT;
+        float v = 0.0f;
+        if (which < 2) {
+            const int64_t mb = (m0 >> 7) + which;
+            if (mb * 128 < p.M) v = p.sa[mb * KT + kb];
+        } else {
+            const int64_t nb = (n0 >> 7) + (which - 2);
+            if (nb * 128 < p.N) v = p.sb[nb * KT + kb];
         }
+        sscale[i] = v;
     }
+    const float* const fa_row = sscale + wm * KT;
+    const float* const fb_row = sscale + (2 + (wn >> 1)) * KT;
 
-    f32x16 acc[4][4];  // [n block][m block]
+    f32x16 acc[2][4];  // [n block][m block]
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    load_tile_lds(smem, p.a, m0, p.M, p.K, 0, wave, lane);
-    load_tile_lds(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
+    load_tile_lds8(smem, p.a, m0, p.M, p.K, 0, wave, lane);
+    load_tile_lds8(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
+    float f_prev = 0.0f;
     for (int kt = 0; kt < KT; ++kt) {
         const uint8_t* cur = smem + (kt & 1) * STAGE_BYTES;
         if (kt + 1 < KT) {
             uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE_BYTES;
-            load_tile_lds(nxt, p.a, m0, p.M, p.K, (int64_t)(kt + 1) * BK, wave, lane);
-            load_tile_lds(nxt + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 1) * BK, wave, lane);
+            load_tile_lds8(nxt, p.a, m0, p.M, p.K, (int64_t)(kt + 1) * BK, wave, lane);
+            load_tile_lds8(nxt + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 1) * BK, wave, lane);
         }
-        const uint8_t* lA = cur;
-        const uint8_t* lB = cur + TILE_BYTES;
-        {
-            // Promote this 128-wide K block with its own scale. The wave's
-            // 128 x 128 sub-tile lies inside one 128 x 128 scale block of
-            // each operand, so the factor is uniform over the wave.
-            const float f = sscale[wm * KT + kt] * sscale[(2 + wn) * KT + kt];
-            i32x8 fa0[4], fa1[4];
+        const float f = fa_row[kt] * fb_row[kt];
+        if (f != 0.0f) {  // wave-uniform
+            const float r = f_prev / f;
+            const uint8_t* a_buf = cur;
+            const uint8_t* b_buf = cur + TILE_BYTES;
+            Frags8 f0, f1;
+            read_slice8(f0, a_buf, b_buf, 0, wm, wn, lane);
+            // Slice 0: slot s = 4 i + j rescales block (i, j) and issues its
+            // MFMA; slots 2..7 also read slice 1's fragments into the
+            // registers slice 0 has finished with (b[0] then the a[j] in the
+            // order slice 1 first needs them).
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                fa0[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), 0, lane);
-                fa1[j] = read_frag(lA, wm * 128 + j * 32 + (lane & 31), 1, lane);
+            for (int s8 = 0; s8 < 8; ++s8) {
+                const int i = s8 >> 2, j = s8 & 3;
+                if (s8 == 2) f1.b[0] = read_frag(b_buf, wn * 64 + (lane & 31), 1, lane);
+                if (s8 >= 3 && s8 <= 6) f1.a[s8 - 3] = read_frag(a_buf, wm * 128 + (s8 - 3) * 32 + (lane & 31), 1, lane);
+                if (s8 == 7) f1.b[1] = read_frag(b_buf, wn * 64 + 32 + (lane & 31), 1, lane);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] *= r;
+                acc[i][j] = mfma(f0.b[i], f0.a[j], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const i32x8 fb0 = read_frag(lB, wn * 128 + i * 32 + (lane & 31), 0, lane);
-                const i32x8 fb1 = read_frag(lB, wn * 128 + i * 32 + (lane & 31), 1, lane);
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f32x16 t = {};
-                    t = mfma(fb0, fa0[j], t);
-                    t = mfma(fb1, fa1[j], t);
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(t[v], f, acc[i][j][v]);
-                }
-            }
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(f1.b[i], f1.a[j], acc[i][j]);
+            f_prev = f;
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
-    epilogue<MODE>(acc, p, m0, n0, smem, wave, wm, wn, lane);
+    // Epilogue: out = acc * f_last in bf16. A lane holds 4 consecutive
+    // columns of one row per (block, register quad): one 8-byte store each;
+    // the 8 stores of a block write whole 64-byte row segments, which the L2
+    // merges.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int64_t n = n0 + wn * 64 + i * 32 + vq * 8 + (lane >> 5) * 4;
+                const f32x16& a = acc[i][j];
+                const uint2 o = make_uint2(pack_bf16(a[4 * vq] * f_prev, a[4 * vq + 1] * f_prev),
+                                           pack_bf16(a[4 * vq + 2] * f_prev, a[4 * vq + 3] * f_prev));
+                if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
+            }
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -1189,7 +1241,7 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     } else if (mode == gemm::ROWCOL)
         gemm::gemm_rowcol_kernel<<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
     else
-        gemm::gemm_fp8_kernel<gemm::BLOCKWISE><<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
+        gemm::gemm_bw8_kernel<<<grid, gemm::NT8, 0, (hipStream_t)stream>>>(p);
     return check_launch(who);
 }
 

@@ -162,6 +162,55 @@ def test_blockwise_gemm_reference_harness(O, dev, m, n, k):
     assert np.all(np.abs(got - expected) <= np.abs(expected) * 2 ** -8 + 1e-3 * np.abs(expected).max())
 
 
+def _blockwise_check(got, expected):
+    got = got.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rel = np.linalg.norm(got - expected) / np.linalg.norm(expected)
+    assert rel < 0.004, rel
+    assert np.all(np.abs(got - expected) <= np.abs(expected) * 2 ** -8 + 1e-3 * np.abs(expected).max())
+
+
+@pytest.mark.parametrize("m,n,k", [(1536, 4096, 12288), (1536, 12288, 4096), (10800, 4096, 4096)])
+def test_blockwise_gemm_decoder_shapes(O, dev, m, n, k):
+    """The decoder's projection shapes (pixelumm_decoder/model.py:43-53: q/o/gate/up
+    and down, K 4096 and 12288), with activation K blocks whose magnitudes differ
+    by up to 2^16 and one all-zero K block, so the per-K-block promotion sees
+    widely different factors. Row blocks 0 and last against the oracle."""
+    print(f"case blockwise decoder gemm {m}x{n}x{k}", flush=True)
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn(m, k, generator=g)
+    b = torch.randn(n, k, generator=g)
+    gain = 2.0 ** torch.randint(-8, 9, (k // 128,), generator=g).float()
+    a = a * gain.repeat_interleave(128)[None, :]
+    a[:, 256:384] = 0.0
+    qa, sa = pf._quantize_blockwise(a.to(torch.bfloat16).to(dev))
+    qb, sb = pf._quantize_blockwise(b.to(torch.bfloat16).to(dev))
+    got = pf.load_extension().gemm(qa, qb, sa, sb)
+    last = (m - 1) // 128
+    rows = list(range(0, 128)) + list(range(last * 128, m))
+    expected = O.blockwise_gemm_reference(u8(qa)[rows], sa.cpu().numpy()[[0, last]], u8(qb), sb.cpu().numpy())
+    _blockwise_check(got[rows], expected)
+
+
+def test_blockwise_gemm_zero_block_factors(O, dev):
+    """Block factors of 0 (an activation K block and a weight K block given scale 0
+    by the caller) contribute nothing; the other blocks are promoted as usual."""
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator().manual_seed(12)
+    a = torch.randn(300, 1024, generator=g).to(torch.bfloat16)
+    b = torch.randn(384, 1024, generator=g).to(torch.bfloat16)
+    qa, sa = pf._quantize_blockwise(a.to(dev))
+    qb, sb = pf._quantize_blockwise(b.to(dev))
+    sa[:, 1] = 0.0
+    sa[2, 0] = 0.0
+    sb[0, 3] = 0.0
+    sb[:, 7] = 0.0
+    got = pf.load_extension().gemm(qa, qb, sa, sb)
+    expected = O.blockwise_gemm_reference(u8(qa), sa.cpu().numpy(), u8(qb), sb.cpu().numpy())
+    _blockwise_check(got, expected)
+
+
 def test_blockwise_gemm_contract_errors(dev):
     pf = pkg_module("pixelumm_fp8")
     ext = pf.load_extension()
