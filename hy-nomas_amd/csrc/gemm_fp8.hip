@@ -242,171 +242,6 @@ HN_DEVICE void epilogue(f32x16 (&acc)[4][4], const Params& p, int64_t m0, int64_
 }
 
 // ---------------------------------------------------------------------------
-// Blockwise-scaled kernel, 8 waves: a 512-thread workgroup owns a 256 x 256
-// output tile; wave w owns rows 128 (w % 2) .. + 127 and columns 64 (w / 2)
-// .. + 63, i.e. 4 x 2 MFMA blocks of 32 x 32 (128 fp32 accumulators per
-// lane, held in VGPRs), two waves per SIMD. K advances 128 bytes per step
-// through two LDS stages (A and B tiles, 2 x 64 KB): while the MFMAs consume
-// stage s, the next step's loads land in stage s ^ 1.
-//
-// Scale promotion without a second accumulator set: the wave's sub-tile lies
-// inside one 128 x 128 scale block of each operand, so K block kt has one
-// factor f_kt = sa[mb][kt] * sb[nb][kt] for the whole sub-tile. The
-// accumulators are kept in units of the current block's factor:
-//     acc_kt = acc_(kt-1) * (f_(kt-1) / f_kt) + A_kt B_kt^T,  out = acc * f_last,
-// which is sum_kt f_kt A_kt B_kt^T up to fp32 rounding of the rescale (one
-// multiply per accumulator per K block, ~2^-24 relative each). A block with
-// f_kt = 0 contributes nothing and is skipped, so f is never divided by 0.
-// The rescale of an MFMA block is issued right before that block's first
-// MFMA of the step, so it runs beside the previous block's MFMA.
-constexpr int NT8 = 512;
-
-// Direct global -> LDS loads of one 256 x 128 operand tile by 8 waves: wave w
-// fills the 1 KB regions 4 w .. 4 w + 3 (rows 32 w .. 32 w + 31), lane l at
-// row l / 8 of its region, physical chunk l % 8 (the logical chunk the
-// swizzle puts there). Rows past the operand's end are clamped to its last
-// row: in bounds, never stored.
-HN_DEVICE void load_tile_lds8(uint8_t* lds_tile, const uint8_t* __restrict__ base, int64_t row0, int64_t rows,
-                              int64_t K, int64_t k0, int wave, int lane) {
-    const uint32_t tile_addr = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int rgn = wave * 4 + i;
-        const int r = rgn * 8 + (lane >> 3);
-        const int c = swz_pos(r, lane & 7);  // the swizzle is an involution
-        int64_t row = row0 + r;
-        row = row < rows ? row : rows - 1;
-        dma_16B(base + row * K + k0 + (c << 4), __builtin_amdgcn_readfirstlane(tile_addr + rgn * 1024));
-    }
-}
-
-// The fragments of one 64-byte K slice for the wave's 128 x 64 sub-tile.
-struct Frags8 {
-    i32x8 b[2];
-    i32x8 a[4];
-};
-
-HN_DEVICE void read_slice8(Frags8& f, const uint8_t* a_buf, const uint8_t* b_buf, int kh, int wm, int wn, int lane) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) f.b[i] = read_frag(b_buf, wn * 64 + i * 32 + (lane & 31), kh, lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) f.a[j] = read_frag(a_buf, wm * 128 + j * 32 + (lane & 31), kh, lane);
-}
-
-__global__ __launch_bounds__(NT8, 1) void gemm_bw8_kernel(Params p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE_BYTES];
-    // the tile's scale rows: [2 m blocks][KT] then [2 n blocks][KT]
-    __shared__ float sscale[4 * kMaxKT];
-
-    // Tile order. Workgroup ids are dealt round-robin to the 8 XCDs, each with
-    // its own L2, so id % 8 selects a contiguous range of work items for that
-    // XCD. Work items are laid out in groups of GROUP_M tile rows, walking N
-    // inside a group: the tiles an XCD runs at once then share their A and B
-    // panels in that L2.
-    const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
-    if (w >= p.tiles_m * p.tiles_n) return;
-    const int per_group = GROUP_M * p.tiles_n;
-    const int first_m = (w / per_group) * GROUP_M;
-    const int gm = min(GROUP_M, p.tiles_m - first_m);
-    const int tm = first_m + (w % per_group) % gm;
-    const int tn = (w % per_group) / gm;
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave & 1, wn = wave >> 1;  // rows 128 wm .., columns 64 wn ..
-    const int KT = (int)(p.K / BK);
-
-    // Blocks wholly past M or N get factor 0: skipped, never stored.
-    for (int i = threadIdx.x; i < 4 * KT; i += NT8) {
-        const int which = i / KT, kb = i % KT;
-        float v = 0.0f;
-        if (which < 2) {
-            const int64_t mb = (m0 >> 7) + which;
-            if (mb * 128 < p.M) v = p.sa[mb * KT + kb];
-        } else {
-            const int64_t nb = (n0 >> 7) + (which - 2);
-            if (nb * 128 < p.N) v = p.sb[nb * KT + kb];
-        }
-        sscale[i] = v;
-    }
-    const float* const fa_row = sscale + wm * KT;
-    const float* const fb_row = sscale + (2 + (wn >> 1)) * KT;
-
-    f32x16 acc[2][4];  // [n block][m block]
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    load_tile_lds8(smem, p.a, m0, p.M, p.K, 0, wave, lane);
-    load_tile_lds8(smem + TILE_BYTES, p.b, n0, p.N, p.K, 0, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    float f_prev = 0.0f;
-    for (int kt = 0; kt < KT; ++kt) {
-        const uint8_t* cur = smem + (kt & 1) * STAGE_BYTES;
-        if (kt + 1 < KT) {
-            uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE_BYTES;
-            load_tile_lds8(nxt, p.a, m0, p.M, p.K, (int64_t)(kt + 1) * BK, wave, lane);
-            load_tile_lds8(nxt + TILE_BYTES, p.b, n0, p.N, p.K, (int64_t)(kt + 1) * BK, wave, lane);
-        }
-        const float f = fa_row[kt] * fb_row[kt];
-        if (f != 0.0f) {  // wave-uniform
-            const float r = f_prev / f;
-            const uint8_t* a_buf = cur;
-            const uint8_t* b_buf = cur + TILE_BYTES;
-            Frags8 f0, f1;
-            read_slice8(f0, a_buf, b_buf, 0, wm, wn, lane);
-            // Slice 0: slot s = 4 i + j rescales block (i, j) and issues its
-            // MFMA; slots 2..7 also read slice 1's fragments into the
-            // registers slice 0 has finished with (b[0] then the a[j] in the
-            // order slice 1 first needs them).
-#pragma unroll
-            for (int s8 = 0; s8 < 8; ++s8) {
-                const int i = s8 >> 2, j = s8 & 3;
-                if (s8 == 2) f1.b[0] = read_frag(b_buf, wn * 64 + (lane & 31), 1, lane);
-                if (s8 >= 3 && s8 <= 6) f1.a[s8 - 3] = read_frag(a_buf, wm * 128 + (s8 - 3) * 32 + (lane & 31), 1, lane);
-                if (s8 == 7) f1.b[1] = read_frag(b_buf, wn * 64 + 32 + (lane & 31), 1, lane);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][j][v] *= r;
-                acc[i][j] = mfma(f0.b[i], f0.a[j], acc[i][j]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(f1.b[i], f1.a[j], acc[i][j]);
-            f_prev = f;
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-    }
-
-    // Epilogue: out = acc * f_last in bf16. A lane holds 4 consecutive
-    // columns of one row per (block, register quad): one 8-byte store each;
-    // the 8 stores of a block write whole 64-byte row segments, which the L2
-    // merges.
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-#pragma unroll
-            for (int vq = 0; vq < 4; ++vq) {
-                const int64_t n = n0 + wn * 64 + i * 32 + vq * 8 + (lane >> 5) * 4;
-                const f32x16& a = acc[i][j];
-                const uint2 o = make_uint2(pack_bf16(a[4 * vq] * f_prev, a[4 * vq + 1] * f_prev),
-                                           pack_bf16(a[4 * vq + 2] * f_prev, a[4 * vq + 3] * f_prev));
-                if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
-            }
-        }
-}
-
-// ---------------------------------------------------------------------------
 // Row/column-scaled kernel: 128-byte K steps through five single-operand LDS
 // buffers.
 //
@@ -511,6 +346,233 @@ HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) {
     tm = g;
     tn = p.tn_full;
     return true;
+}
+
+// ---------------------------------------------------------------------------
+// Blockwise-scaled kernel, 8 waves: a 512-thread workgroup owns a 256 x 256
+// output tile; wave w owns rows 128 (w % 2) .. + 127 and columns 64 (w / 2)
+// .. + 63, i.e. 4 x 2 MFMA blocks of 32 x 32 (128 fp32 accumulators per
+// lane, held in VGPRs), two waves per SIMD. The K pipeline is the row/column
+// kernel's: five single-operand 32 KB buffers, L(2 s) = A(s) and L(2 s + 1)
+// = B(s) in buffer L % 5; step k's half 0 runs the MFMAs of K slice (k, 0)
+// beside the reads of slice (k, 1); a mid-step wait and barrier make step
+// k + 1's buffers complete and free step k's; half 1 runs slice (k, 1)
+// beside the reads of slice (k + 1, 0) and the DMAs of B(k + 2) and
+// A(k + 3) into step k's buffers, one 1 KB DMA per MFMA (each wave fills 4
+// of a buffer's 32 regions).
+//
+// Scale promotion without a second accumulator set: the wave's sub-tile lies
+// inside one 128 x 128 scale block of each operand, so K block k has one
+// factor f_k = sa[mb][k] * sb[nb][k] for the whole sub-tile. The accumulators
+// are kept in units of the current block's factor:
+//     acc_k = acc_(k-1) * (f_(k-1) / f_k) + A_k B_k^T,  out = acc * f_last,
+// which is sum_k f_k A_k B_k^T up to fp32 rounding of the rescale (one
+// multiply per accumulator per K block, ~2^-24 relative each). A block with
+// f_k = 0 contributes nothing: its MFMAs are skipped (the wave still takes
+// part in every read, DMA and barrier), so f is never divided by 0. The
+// rescale of an MFMA block is issued right before that block's first MFMA of
+// the step, beside the previous block's MFMA.
+constexpr int NT8 = 512;
+
+// Per-lane offsets of a wave's four 1 KB regions of one 256 x 128 buffer
+// (region q: 8 rows of 128 bytes; lane l lands at row 32 w + 8 q + l / 8,
+// physical chunk l % 8, and fetches the logical chunk the swizzle puts
+// there). Rows past the operand's end are clamped to its last row: in
+// bounds, never stored.
+HN_DEVICE void buffer_offsets8(uint32_t (&off)[4], int64_t row0, int64_t rows, int64_t K, int wave, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = (wave * 4 + q) * 8 + (lane >> 3);
+        const int c = swz_pos(r, lane & 7);
+        const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+        off[q] = (uint32_t)((row - row0) * K + (c << 4));
+    }
+}
+
+// The fragments of one 64-byte K slice for the wave's 128 x 64 sub-tile.
+struct Frags8 {
+    i32x8 b[2];
+    i32x8 a[4];
+};
+
+// Fragment t (0..5) of a slice: weight blocks b[0], b[1], then activation
+// blocks a[0..3].
+HN_DEVICE void read_frag8(Frags8& f, int t, const uint8_t* a_buf, const uint8_t* b_buf, int kh, int wm, int wn,
+                          int lane) {
+    if (t < 2) f.b[t] = read_frag(b_buf, wn * 64 + t * 32 + (lane & 31), kh, lane);
+    else f.a[t - 2] = read_frag(a_buf, wm * 128 + (t - 2) * 32 + (lane & 31), kh, lane);
+}
+
+__global__ __launch_bounds__(NT8, 1) void gemm_bw8_kernel(Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[R_SMEM];
+
+    // Tile order. Workgroup ids are dealt round-robin to the 8 XCDs, each with
+    // its own L2, so id % 8 selects a contiguous range of work items for that
+    // XCD. Work items are laid out in groups of GROUP_M tile rows, walking N
+    // inside a group: the tiles an XCD runs at once then share their A and B
+    // panels in that L2.
+    const int w = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+    if (w >= p.tiles_m * p.tiles_n) return;
+    const int per_group = GROUP_M * p.tiles_n;
+    const int first_m = (w / per_group) * GROUP_M;
+    const int gm = min(GROUP_M, p.tiles_m - first_m);
+    const int tm = first_m + (w % per_group) % gm;
+    const int tn = (w % per_group) / gm;
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1, wn = wave >> 1;  // rows 128 wm .., columns 64 wn ..
+    const int KT = (int)(p.K / BK);
+    const uint8_t* const a_tile = p.a + m0 * p.K;
+    const uint8_t* const b_tile = p.b + n0 * p.K;
+    uint32_t off_a[4], off_b[4];
+    buffer_offsets8(off_a, m0, p.M, p.K, wave, lane);
+    buffer_offsets8(off_b, n0, p.N, p.K, wave, lane);
+    const uint32_t lds_base = lds_addr(smem) + wave * 4 * 1024;
+
+    // Block factors of this wave's sub-tile (0 for a sub-tile past M or N:
+    // its MFMAs are skipped and it is never stored).
+    // The scale rows are read through the constant address space: wave-uniform
+    // loads of memory the kernel never writes become scalar loads, outside
+    // the vector-memory counter that the DMA waits count.
+    typedef const __attribute__((address_space(4))) float cfloat;
+    const int64_t mb = (m0 >> 7) + wm, nb = (n0 >> 7) + (wn >> 1);
+    const bool live = mb * 128 < p.M && nb * 128 < p.N;
+    cfloat* const sa_row = (cfloat*)p.sa + (live ? mb : 0) * KT;
+    cfloat* const sb_row = (cfloat*)p.sb + (live ? nb : 0) * KT;
+    auto factor = [&](int k) { return live ? sa_row[k] * sb_row[k] : 0.0f; };
+
+    f32x16 acc[2][4];  // [n block][m block]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    auto a_buf = [&](int s) { return smem + ((2 * s) % R_BUFS) * R_BUF; };
+    auto b_buf = [&](int s) { return smem + ((2 * s + 1) % R_BUFS) * R_BUF; };
+    auto issue_a = [&](int s) {
+        const uint32_t dst = lds_base + ((2 * s) % R_BUFS) * R_BUF;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dma_16B_sbase(a_tile + (int64_t)s * BK, off_a[q], dst + q * 1024);
+    };
+    auto issue_b = [&](int s) {
+        const uint32_t dst = lds_base + ((2 * s + 1) % R_BUFS) * R_BUF;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dma_16B_sbase(b_tile + (int64_t)s * BK, off_b[q], dst + q * 1024);
+    };
+    // Prologue: L(0) .. L(4), then wait for step 0 (L(0), L(1)).
+    issue_a(0);
+    issue_b(0);
+    if (KT > 1) {
+        issue_a(1);
+        issue_b(1);
+        if (KT > 2) {
+            issue_a(2);
+            asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        }
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+
+    Frags8 cur, nxt;
+#pragma unroll
+    for (int t = 0; t < 6; ++t) read_frag8(cur, t, a_buf(0), b_buf(0), 0, wm, wn, lane);
+    float f_prev = 0.0f;
+
+    // A block whose factor is 0 contributes nothing: its fragments are zeroed
+    // (so its MFMAs add 0) and the rescale is 1 (the rare wave-uniform branch
+    // keeps one copy of the step's code).
+    auto zero = [&](Frags8& f) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) f.b[t] = i32x8{};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) f.a[t] = i32x8{};
+    };
+    // half 0 of step k: slot s = 4 i + j rescales block (i, j) by r and
+    // issues its MFMA on slice (k, 0); slots 0..5 also read fragment s of
+    // slice (k, 1).
+    auto half0 = [&](int k, float r) {
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            const int i = s8 >> 2, j = s8 & 3;
+            if (s8 < 6) read_frag8(nxt, s8, a_buf(k), b_buf(k), 1, wm, wn, lane);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] *= r;
+            acc[i][j] = mfma(cur.b[i], cur.a[j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // half 1 of step k: MFMAs on slice (k, 1); with NEXT, slots 0..5 read
+    // fragment s of slice (k + 1, 0); with DB, slots 0..3 issue B(k + 2)'s
+    // regions and, with DA, slots 4..7 A(k + 3)'s.
+    auto half1 = [&](int k, auto next_tag, auto db_tag, auto da_tag) {
+        constexpr bool NEXT = decltype(next_tag)::value;
+        constexpr bool DB = decltype(db_tag)::value, DA = decltype(da_tag)::value;
+        const uint32_t db = lds_base + ((2 * (k + 2) + 1) % R_BUFS) * R_BUF;
+        const uint32_t da = lds_base + ((2 * (k + 3)) % R_BUFS) * R_BUF;
+        const uint8_t* bsrc = b_tile + (int64_t)(k + 2) * BK;
+        const uint8_t* asrc = a_tile + (int64_t)(k + 3) * BK;
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) {
+            const int i = s8 >> 2, j = s8 & 3;
+            if (NEXT && s8 < 6) read_frag8(cur, s8, a_buf(k + 1), b_buf(k + 1), 0, wm, wn, lane);
+            acc[i][j] = mfma(nxt.b[i], nxt.a[j], acc[i][j]);
+            if (DB && s8 < 4) dma_16B_sbase(bsrc, off_b[s8], db + s8 * 1024);
+            if (DA && s8 >= 4) dma_16B_sbase(asrc, off_a[s8 - 4], da + (s8 - 4) * 1024);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    // One step k before the last: half 0, the mid-step wait (step k + 1's
+    // buffers landed in this wave: in flight after them at most A(k + 2),
+    // issued in half 1 of step k - 1 or the prologue) and barrier (every
+    // wave; step k's buffers free), half 1 with the DMAs DB / DA.
+    float f = factor(0);
+    auto step = [&](int k, auto next_tag, auto db_tag, auto da_tag) {
+        const float f_next = decltype(next_tag)::value ? factor(k + 1) : 0.0f;  // scalar loads, issued early
+        if (f == 0.0f) zero(cur);
+        half0(k, f != 0.0f ? f_prev / f : 1.0f);
+        if (f == 0.0f) zero(nxt);
+        if (decltype(next_tag)::value) {
+            if (decltype(db_tag)::value) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+        half1(k, next_tag, db_tag, da_tag);
+        if (f != 0.0f) f_prev = f;
+        f = f_next;
+    };
+    int k = 0;
+    for (; k + 3 < KT; ++k) step(k, T{}, T{}, T{});
+    if (k + 2 < KT) step(k++, T{}, T{}, F{});
+    if (k + 1 < KT) step(k++, T{}, F{}, F{});
+    step(k, F{}, F{}, F{});  // k = KT - 1: nothing further to read or issue
+
+    // Epilogue: out = acc * f_last in bf16. A lane holds 4 consecutive
+    // columns of one row per (block, register quad): one 8-byte store each;
+    // the 8 stores of a block write whole 64-byte row segments, which the L2
+    // merges.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int64_t n = n0 + wn * 64 + i * 32 + vq * 8 + (lane >> 5) * 4;
+                const f32x16& a = acc[i][j];
+                const uint2 o = make_uint2(pack_bf16(a[4 * vq] * f_prev, a[4 * vq + 1] * f_prev),
+                                           pack_bf16(a[4 * vq + 2] * f_prev, a[4 * vq + 3] * f_prev));
+                if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
+            }
+        }
 }
 
 __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
