@@ -15,11 +15,19 @@
 //   valu N          N v_fma_f32 per slot, no MFMA
 //   mfma+N          1 MFMA + N v_fma_f32 in the same wave
 //   split N         even waves MFMA only, odd waves N v_fma_f32 only
-//   tile            the attention's tile: 16 step-A slots (MFMA + 2 fma,
-//                   2 exp, 1 cvt_pk_f16, 1 dot2), 8 K-write slots (MFMA +
-//                   fp8 cvt, 2 mul, cvt_pk_bf16, max3), 8 V-write slots (the
-//                   same + 2 unpack + cvt_pkrtz); each MFMA's A operand read
-//                   from LDS two slots ahead, as the kernel does.
+//   tile            the attention's tile in the kernel's order: 8 step-A
+//                   slots (MFMA + 2 fma, 2 exp, 1 cvt_pk_f16, 1 dot2), 8
+//                   K-write slots (MFMA + fp8 cvt, 2 mul, cvt_pk_bf16, max3),
+//                   8 step-A slots, 8 V-write slots (the K-write work + 2
+//                   unpack + cvt_pkrtz); each MFMA's A operand read from LDS
+//                   two slots ahead, as the kernel does.
+//   tile+barrier    the same with a workgroup barrier after every tile, as
+//                   the kernel has (its waves then run each phase together).
+//   tile+barrier, rotated
+//                   the same, with the waves of the workgroup's upper half
+//                   (the second wave of each SIMD) starting 8 slots later in
+//                   the tile's order, so one wave of a SIMD is in a step-A
+//                   phase while the other is in a write phase.
 //
 // Build: hy-nomas_amd/build.py (build_probes) -> hy-nomas_amd/probes/issue_rates
 // Run:   hy-nomas_amd/probes/issue_rates   (one GPU, about a second)
@@ -44,7 +52,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int SLOTS = 32;  // slots per loop iteration (one attention tile per wave)
 constexpr int LDS_BYTES = 96 * 1024;
 
-enum Pattern { MFMA = 0, VALU = 1, MFMA_VALU = 2, SPLIT = 3, TILE = 4 };
+enum Pattern { MFMA = 0, VALU = 1, MFMA_VALU = 2, SPLIT = 3, TILE = 4, TILE_BAR = 5, TILE_BAR_ROT = 6 };
 
 __device__ __forceinline__ void fma_op(float& x, float c) { asm volatile("v_fma_f32 %0, %0, %1, 0.5" : "+v"(x) : "v"(c)); }
 
@@ -72,8 +80,10 @@ __device__ __forceinline__ void tile_valu(int k, float (&x)[12], float c, uint32
 }
 
 // The slot loop of one wave role (compile-time: MFMA issued, VALU pattern).
-// VK: 0 none, 1 NV x v_fma_f32, 2 the attention slot mix (with LDS operands).
-template <bool MF, int VK, int NV>
+// VK: 0 none, 1 NV x v_fma_f32, 2 the attention slot mix (with LDS operands);
+// BAR: a workgroup barrier after each 32-slot tile; ROT: the tile's slot
+// kinds taken 8 slots later.
+template <bool MF, int VK, int NV, bool BAR = false, bool ROT = false>
 __device__ float slot_loop(int iters, const uint8_t* lds) {
     f32x16 acc[2];
     for (int a = 0; a < 2; ++a)
@@ -104,9 +114,13 @@ __device__ float slot_loop(int iters, const uint8_t* lds) {
 #pragma unroll
                 for (int j = 0; j < NV; ++j) fma_op(x[j % 12], c);
             }
-            if (VK == 2) tile_valu(s < 16 ? 0 : s < 24 ? 1 : 2, x, c, w);
+            if (VK == 2) {
+                const int k = ROT ? (s + 8) & 31 : s;  // kernel order: A, K write, A, V write
+                tile_valu((k & 8) == 0 ? 0 : (k & 16) == 0 ? 1 : 2, x, c, w);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (BAR) __syncthreads();
     }
     float sum = 0.0f;
     for (int a = 0; a < 2; ++a)
@@ -125,6 +139,11 @@ __global__ void issue_kernel(int iters, float* out) {
     else if (PAT == VALU) sum = slot_loop<false, 1, NV>(iters, lds);
     else if (PAT == MFMA_VALU) sum = slot_loop<true, 1, NV>(iters, lds);
     else if (PAT == TILE) sum = slot_loop<true, 2, 0>(iters, lds);
+    else if (PAT == TILE_BAR) sum = slot_loop<true, 2, 0, true>(iters, lds);
+    else if (PAT == TILE_BAR_ROT) {
+        if ((__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2) & 1) sum = slot_loop<true, 2, 0, true, true>(iters, lds);
+        else sum = slot_loop<true, 2, 0, true>(iters, lds);
+    }
     else if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 1) sum = slot_loop<false, 1, NV>(iters, lds);
     else sum = slot_loop<true, 0, 0>(iters, lds);  // SPLIT: even waves MFMA, odd waves VALU
     out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
@@ -173,6 +192,8 @@ int main() {
         line("mfma+8", run<MFMA_VALU, 8>(threads, out), true);
         if (wps > 1) line("split 8 (even: mfma, odd: 8 valu)", run<SPLIT, 8>(threads, out), true, 0.5);
         line("tile (attention slot mix + LDS reads)", run<TILE, 0>(threads, out), true);
+        line("tile + barrier per tile", run<TILE_BAR, 0>(threads, out), true);
+        if (wps > 1) line("tile + barrier, upper waves rotated", run<TILE_BAR_ROT, 0>(threads, out), true);
     }
     CHECK(hipFree(out));
     return 0;
