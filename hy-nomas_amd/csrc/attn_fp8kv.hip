@@ -164,7 +164,14 @@ HN_DEVICE uint32_t pack_f16_of_bf16(float a, float b) { return bf16x2_to_f16x2(p
 // ---------------------------------------------------------------------------
 // Tile loads and LDS writes.
 //
-// K: thread t owns units u = t + NT i (i < KU): key u / 8, 16 dims at 16 (u % 8).
+// K: thread t owns units i < KU: key k_key(t) + NT / 8 i, 16 dims at 16 k_unit(t).
+// In each wave, lane bits 0-1 give the unit's low bits, bit 2 the key's low
+// bit, bit 3 the unit's high bit and bits 4-5 the key's high bits: 16 lanes
+// cover two whole key rows (256 contiguous bytes of the cache), and the
+// 16-byte LDS writes of any 8 consecutive lanes (two keys, rows 272 B apart)
+// fall in 8 different 16-byte bank groups -- a 16-byte LDS write is served 8
+// lanes at a time over 128 bytes of banks, so one key's 8 units 32 B apart
+// would pair up.
 // V^T: thread t (wave w, lane λ) owns key quad qd = λ % 16 (keys quad_key(qd, j),
 // j < 4: the 8-byte half qd % 2 of column unit qd / 2) and the VD dims VD dg ..
 // VD dg + VD - 1 (v_group). Per 8-byte LDS write a 32-lane group covers 2 dim
@@ -175,6 +182,11 @@ HN_DEVICE uint32_t pack_f16_of_bf16(float a, float b) { return bf16x2_to_f16x2(p
 // of key t - 64, into the tile's scale buffer.
 // Validity (MASK): threads 128-191 (wave 2) load the validity byte of key
 // t - 128; the wave's ballot is the tile's validity word.
+
+// Key (within the tile, for i = 0) and unit (16-code run of the key) of
+// thread t's K unit.
+HN_DEVICE uint32_t k_key(uint32_t t) { return 8u * (t >> 6) + 2u * ((t >> 4) & 3u) + ((t >> 2) & 1u); }
+HN_DEVICE uint32_t k_unit(uint32_t t) { return (t & 3u) + 4u * ((t >> 3) & 1u); }
 
 // Key (0..63) of entry j (0..3) of quad qd.
 HN_DEVICE int quad_key(int qd, int j) {
@@ -251,7 +263,7 @@ HN_DEVICE LaneOffs<NW> lane_offsets(const Params& p) {
     const uint32_t t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < Shape<NW>::KU; ++i)
-        o.k[i] = ((t >> 3) + (uint32_t)(Shape<NW>::NT / 8) * i) * (uint32_t)p.cs1 + (t & 7u) * 16u;
+        o.k[i] = (k_key(t) + (uint32_t)(Shape<NW>::NT / 8) * i) * (uint32_t)p.cs1 + k_unit(t) * 16u;
     const int qd = t & 15, dg = v_group<NW>();
 #pragma unroll
     for (int j = 0; j < 4; ++j) o.v[j] = (uint32_t)quad_key(qd, j) * (uint32_t)p.cs1 + (uint32_t)(Shape<NW>::VD * dg);
@@ -342,8 +354,8 @@ HN_DEVICE void store_k_part(const CacheRegs<NW>& r, uint8_t* st, int i, const fl
         kd[(cc >> 1) & 3] = pack_bf16(a[0] * ks[un], a[1] * ks[un]);
     }
     if (((c + CP) & 7) == 0) {
-        const int u = threadIdx.x + Shape<NW>::NT * un;
-        *reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32 + ((c + CP - 8) >> 3) * 16) =
+        const uint32_t key = k_key(threadIdx.x) + (Shape<NW>::NT / 8) * un;
+        *reinterpret_cast<uint4*>(st + key * KROW + k_unit(threadIdx.x) * 32 + ((c + CP - 8) >> 3) * 16) =
             make_uint4(kd[0], kd[1], kd[2], kd[3]);
     }
 }
@@ -352,7 +364,7 @@ HN_DEVICE void store_k_part(const CacheRegs<NW>& r, uint8_t* st, int i, const fl
 template <int NW>
 HN_DEVICE void k_scales(const float* sb, float (&ks)[Shape<NW>::KU]) {
 #pragma unroll
-    for (int i = 0; i < Shape<NW>::KU; ++i) ks[i] = sb[(threadIdx.x >> 3) + (Shape<NW>::NT / 8) * i];
+    for (int i = 0; i < Shape<NW>::KU; ++i) ks[i] = sb[k_key(threadIdx.x) + (Shape<NW>::NT / 8) * i];
 }
 
 // Dequantized V^T write, part i (0..7): quad key j = i / 2, dims VD/2 (i % 2)
@@ -431,12 +443,12 @@ HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first,
     }
 #pragma unroll
     for (int i = 0; i < Shape<NW>::KU; ++i) {
-        const int u = t + Shape<NW>::NT * i;
-        const int j = min(u >> 3, count - 1);
-        const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + (u & 7) * 16;
+        const int key = (int)k_key(t) + (Shape<NW>::NT / 8) * i, unit = (int)k_unit(t);
+        const int j = min(key, count - 1);
+        const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + unit * 16;
         const uint4 lo = *reinterpret_cast<const uint4*>(src);
         const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
-        uint4* dst = reinterpret_cast<uint4*>(st + (u >> 3) * KROW + (u & 7) * 32);
+        uint4* dst = reinterpret_cast<uint4*>(st + key * KROW + unit * 32);
         dst[0] = lo;
         dst[1] = hi;
     }
