@@ -16,7 +16,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-seconds S]
 ``--only`` runs one workload (for per-kernel counter passes): ``attn`` config 3,
 ``decode`` 128 queries over the same 86 400-key cache, ``blockwise`` the decoder
 layer's five blockwise-scaled FP8 GEMMs; ``copy`` is a plain 1 GiB device copy
-used to calibrate the FETCH_SIZE / WRITE_SIZE counters.
+used to calibrate the FETCH_SIZE / WRITE_SIZE counters; ``vendor`` times
+hipBLASLt's FP8 GEMM (torch._scaled_mm, row-wise scales, no bias or
+activation) beside this build's on the same operands.
 """
 from __future__ import annotations
 
@@ -105,7 +107,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "linear", "kv", "attn", "decode", "blockwise", "copy", "ar"])
+                    choices=["all", "linear", "kv", "attn", "decode", "blockwise", "copy", "ar", "vendor"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -418,6 +420,25 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
         log(f"KV write {ms * 1e3:.1f} us")
     elif args.only == "blockwise":
         bench_decoder_linears(args, torch, ops, dev, g, log)
+    elif args.only == "vendor":
+        # hipBLASLt (through torch._scaled_mm: out = (a sa) (b sb)^T in bf16)
+        # against hn_gemm_fp8_rowcol without bias or activation, same operands.
+        a = torch.randn(NS_M, NS_K, device=dev, generator=g).to(torch.bfloat16)
+        qa, sa = ops.quantize_rows_fp8(a)
+        settle = clock_settle(lambda: ops.gemm_fp8_rowcol(qa, qa[:NS_K], sa, sa[:NS_K]), args.settle_seconds, torch)
+        log(f"clock settle: {settle['calls']} GEMM calls in {settle['seconds']:.2f} s")
+        for (m, k, n) in ((NS_M, NS_K, NS_N), (C1_M, C1_K, C1_N), (NS_M, NS_N, NS_K)):
+            qa, sa = ops.quantize_rows_fp8(torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16))
+            qb, sb = ops.quantize_rows_fp8((torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16))
+            ours = time_loop(lambda: ops.gemm_fp8_rowcol(qa, qb, sa, sb), args.steps, args.warmup)
+            sa2, sb2 = sa.view(m, 1), sb.view(1, n)
+            theirs = time_loop(lambda: torch._scaled_mm(qa, qb.t(), scale_a=sa2, scale_b=sb2,
+                                                        out_dtype=torch.bfloat16), args.steps, args.warmup)
+            diff = (ops.gemm_fp8_rowcol(qa, qb, sa, sb).float()
+                    - torch._scaled_mm(qa, qb.t(), scale_a=sa2, scale_b=sb2, out_dtype=torch.bfloat16).float())
+            tf = gemm_flops(m, k, n) / 1e9
+            log(f"{m}x{k}x{n}: hn_gemm_fp8_rowcol {ours * 1e3:.1f} us ({tf / ours:.0f} TFLOP/s), "
+                f"hipBLASLt {theirs * 1e3:.1f} us ({tf / theirs:.0f} TFLOP/s), max |diff| {diff.abs().max().item():.3g}")
     elif args.only in ("attn", "decode"):
         lk = ATT_CHUNKS * KV_L
         cache = kvc.make_fp8_kv_block(1, lk, KV_H, KV_D, device=dev)
