@@ -427,7 +427,7 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
         qa, sa = ops.quantize_rows_fp8(a)
         settle = clock_settle(lambda: ops.gemm_fp8_rowcol(qa, qa[:NS_K], sa, sa[:NS_K]), args.settle_seconds, torch)
         log(f"clock settle: {settle['calls']} GEMM calls in {settle['seconds']:.2f} s")
-        for (m, k, n) in ((NS_M, NS_K, NS_N), (C1_M, C1_K, C1_N), (NS_M, NS_N, NS_K)):
+        for (m, k, n) in ((NS_M, NS_K, NS_N), (C1_M, C1_K, C1_N), (NS_M, NS_N, NS_K), (8192, 8192, 8192)):
             qa, sa = ops.quantize_rows_fp8(torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16))
             qb, sb = ops.quantize_rows_fp8((torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16))
             ours = time_loop(lambda: ops.gemm_fp8_rowcol(qa, qb, sa, sb), args.steps, args.warmup)
