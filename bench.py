@@ -223,6 +223,9 @@ def main():
     dec_gbs = attn_unique_bytes(KV_H, 128, lk, KV_D) / (ms_dec * 1e-3) / 1e9
     log(f"decode-style attention (Lq=128) {ms_dec * 1e3:.1f} us ({dec_gbs:.0f} GB/s)")
 
+    # ---------------- the widened rows: fused kernels either side of the path, INT8-compat KV
+    wide_res = bench_widened(args, torch, kvc, ca, dev, g, lib, L, stream_ptr, log)
+
     # ---------------- config 4: one FP8 DiT block over 7 cached chunks + the current one
     blk_res = bench_block(args, torch, cache, dev, g, log)
     del cache, q, qd
@@ -282,11 +285,96 @@ def main():
                       "decode_lq128_gbs": round(dec_gbs, 1),
                       "decode_frac_hbm": round(dec_gbs / HBM_PEAK_GBS, 4)},
         "decoder_blockwise": dec_res,
+        "widened": wide_res,
         "dit_block": blk_res,
         "ar_chunk": ar_res,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result))
+
+
+def bench_widened(args, torch, kvc, ca, dev, g, lib, L, stream_ptr, log):
+    """The kernels beside the hot path, each at the block's shapes:
+    * LayerNorm + adaLN modulate + per-token e4m3 quant of the block input,
+      10800 x 3072 (the input of QKV and of fc1);
+    * QK RMSNorm + RoPE in place on the QKV output with the K/V cache write in
+      the same kernel (the AR write pass), 10800 tokens x 24 heads;
+    * the reference's own INT8 KV format: the config-2 write and the config-3
+      and decode-style attention over an INT8 cache.
+    Short kernels go through the C ABI with preallocated outputs. Algorithmic
+    bytes: LN + quant 2 C + C + 4 per row; QK + write reads q, k, v and the
+    fp32 cos/sin tables, writes q, k, the K/V codes and their scales."""
+    bf, f8 = torch.bfloat16, torch.float8_e4m3fn
+    res = {}
+    x = torch.randn(1, NS_M, NS_K, device=dev, generator=g).to(bf)
+    shift = (torch.randn(1, NS_K, device=dev, generator=g) * 0.1).to(bf)
+    scale = (torch.randn(1, NS_K, device=dev, generator=g) * 0.1).to(bf)
+    qx = torch.empty(NS_M, NS_K, dtype=f8, device=dev)
+    sx = torch.empty(NS_M, dtype=torch.float32, device=dev)
+    ln_args = (x.data_ptr(), NS_M, NS_K, NS_M, shift.data_ptr(), scale.data_ptr(), NS_K, 1e-6, 1e-4,
+               qx.data_ptr(), sx.data_ptr(), stream_ptr)
+    L.check(lib.hn_ln_mod_quantize_fp8(*ln_args), "hn_ln_mod_quantize_fp8")
+    ms = time_loop(lambda: lib.hn_ln_mod_quantize_fp8(*ln_args), args.steps, args.warmup)
+    nbytes = NS_M * NS_K * 3 + NS_M * 4
+    res["ln_mod_quant"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                           "shape": [NS_M, NS_K]}
+    log(f"LayerNorm + modulate + quant {ms * 1e3:.1f} us ({nbytes / (ms * 1e-3) / 1e9:.0f} GB/s)")
+    del x, qx
+
+    H, D = KV_H, KV_D
+    qkv = torch.randn(1, KV_L, 3, H, D, device=dev, generator=g).to(bf)
+    q, k, v = qkv.unbind(2)
+    qw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    kw = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(bf)
+    ang = torch.rand(KV_L, D, device=dev, generator=g) * 6.283
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    cache = kvc.make_fp8_kv_block(1, KV_L, H, D, device=dev)
+    qk_args = (L.HN_KV_FP8, q.data_ptr(), k.data_ptr(), v.data_ptr(), L.strides(q), 1, KV_L, H, D,
+               qw.data_ptr(), kw.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.stride(0), 1e-6,
+               cache["k"].data_ptr(), cache["v"].data_ptr(), L.strides(cache["k"]),
+               cache["k_scale"].data_ptr(), cache["v_scale"].data_ptr(), L.strides(cache["k_scale"]),
+               KV_L, 0, None, stream_ptr)
+    L.check(lib.hn_qk_norm_rope_kv(*qk_args), "hn_qk_norm_rope_kv")
+    ms = time_loop(lambda: lib.hn_qk_norm_rope_kv(*qk_args), args.steps, args.warmup)
+    rows = KV_L * H
+    nbytes = rows * D * 2 * 3 + 2 * KV_L * D * 4 + rows * D * 2 * 2 + rows * D * 2 + rows * 4 * 2
+    res["qk_norm_rope_kv_write"] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                    "shape": [1, KV_L, H, D]}
+    log(f"QK RMSNorm + RoPE + KV write {ms * 1e3:.1f} us ({nbytes / (ms * 1e-3) / 1e9:.0f} GB/s)")
+    del qkv, q, k, v, cache
+
+    # INT8-compat KV (the reference's kv_cache_quantization=int8 format)
+    lk = ATT_CHUNKS * KV_L
+    cache = kvc.make_int8_kv_block(1, lk, H, D, device=dev)
+    gain = torch.empty(H, device=dev).uniform_(0.5, 4.0, generator=g)
+    kb = (torch.randn(1, H, KV_L, D, device=dev, generator=g) * gain[None, :, None, None]).to(bf).transpose(1, 2)
+    vb = (torch.randn(1, H, KV_L, D, device=dev, generator=g) * gain[None, :, None, None]).to(bf).transpose(1, 2)
+    kv_args = (L.HN_KV_INT8, kb.data_ptr(), vb.data_ptr(), L.strides(kb), 1, KV_L, H, D,
+               cache["k"].data_ptr(), cache["v"].data_ptr(), L.strides(cache["k"]),
+               cache["k_scale"].data_ptr(), cache["v_scale"].data_ptr(), L.strides(cache["k_scale"]),
+               lk, (ATT_CHUNKS - 1) * KV_L, None, stream_ptr)
+    L.check(lib.hn_kv_quantize_pair(*kv_args), "hn_kv_quantize_pair")
+    ms_kv = time_loop(lambda: lib.hn_kv_quantize_pair(*kv_args), args.steps, args.warmup)
+    for c in range(ATT_CHUNKS):
+        gain = torch.empty(H, device=dev).uniform_(0.5, 4.0, generator=g)
+        kc = (torch.randn(1, KV_L, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(bf)
+        vc = (torch.randn(1, KV_L, H, D, device=dev, generator=g) * gain[None, None, :, None]).to(bf)
+        kvc.quantize_kv_pair_into(cache, kc, vc, c * KV_L)
+    del kc, vc, kb, vb
+    qa = torch.randn(1, KV_L, H, D, device=dev, generator=g).to(bf)
+    ms_att = time_loop(lambda: ca.chunk_attention(qa, cache, lk, q_pos0=lk - KV_L, chunk_len=KV_L),
+                       max(2, args.steps // 4), max(1, args.warmup // 2))
+    qd = qa[:, :128].contiguous()
+    ms_dec = time_loop(lambda: ca.chunk_attention(qd, cache, lk), args.steps, args.warmup)
+    kv_gbs = kv_write_bytes() / (ms_kv * 1e-3) / 1e9
+    att_tflops = attn_flops(H, KV_L, lk, D) / (ms_att * 1e-3) / 1e12
+    dec_gbs = attn_unique_bytes(H, 128, lk, D) / (ms_dec * 1e-3) / 1e9
+    res["int8_kv"] = {"write_us": round(ms_kv * 1e3, 2), "write_gbs": round(kv_gbs, 1),
+                      "attention_ms": round(ms_att, 4), "attention_tflops": round(att_tflops, 2),
+                      "decode_lq128_us": round(ms_dec * 1e3, 2), "decode_lq128_gbs": round(dec_gbs, 1)}
+    log(f"INT8 KV: write {ms_kv * 1e3:.1f} us ({kv_gbs:.0f} GB/s); chunk attention {ms_att:.3f} ms "
+        f"({att_tflops:.0f} TFLOP/s); decode-style {ms_dec * 1e3:.1f} us ({dec_gbs:.0f} GB/s)")
+    return res
 
 
 # The PixelUMM decoder layer's FP8 linears (pixelumm_decoder/model.py:43-53,

@@ -117,13 +117,25 @@ struct Quot {
     }
 };
 
-HN_DEVICE uint32_t int8_code(float v) {
-    // int8_kv_cache.py:150-157: fp32 round-half-away via floor(v + 0.5) /
-    // ceil(v - 0.5) (each add rounded in fp32), then clamp to +-127.
-    float r = v >= 0.0f ? floorf(v + 0.5f) : ceilf(v - 0.5f);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    return (uint32_t)(int32_t)r & 0xffu;
+// int8_kv_cache.py:150-157: fp32 round-half-away via floor(v + 0.5) /
+// ceil(v - 0.5) (each add rounded in fp32), then clamp to +-127. Round to
+// nearest is symmetric, so v - 0.5 rounds to -(|v| + 0.5) rounded and
+// ceil(v - 0.5) = -floor(|v| + 0.5): the code is sign(v) min(floor(|v| + 0.5),
+// 127) for either sign (-0 and +0 both give 0).
+HN_DEVICE int int8_code_i32(float v) {
+    const float t = fminf(floorf(fabsf(v) + 0.5f), 127.0f);
+    return (int)__builtin_copysignf(t, v);
 }
+
+// Four INT8 codes, packed little-endian into one word: two saturating
+// i32 -> i16 packs (exact: every code is in [-127, 127]) and one byte select.
+HN_DEVICE uint32_t int8_pack4(int a, int b, int c, int d) {
+    const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(a, b));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(c, d));
+    return __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // bytes 0, 2 of lo, then of hi
+}
+
+HN_DEVICE uint32_t int8_code(float v) { return (uint32_t)int8_code_i32(v) & 0xffu; }
 
 // The 8 codes (e4m3 if FP8, else INT8) of one lane's 8 values of a row with
 // quotient d; the quotient form is chosen once for the 8.
@@ -136,12 +148,10 @@ HN_DEVICE uint2 codes8(const float (&f)[8], const Quot& d) {
             out.x = e4m3_encode4(d.at<E>(f[0]), d.at<E>(f[1]), d.at<E>(f[2]), d.at<E>(f[3]));
             out.y = e4m3_encode4(d.at<E>(f[4]), d.at<E>(f[5]), d.at<E>(f[6]), d.at<E>(f[7]));
         } else {
-            out.x = out.y = 0;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                out.x |= int8_code(d.at<E>(f[j])) << (8 * j);
-                out.y |= int8_code(d.at<E>(f[j + 4])) << (8 * j);
-            }
+            out.x = int8_pack4(int8_code_i32(d.at<E>(f[0])), int8_code_i32(d.at<E>(f[1])),
+                               int8_code_i32(d.at<E>(f[2])), int8_code_i32(d.at<E>(f[3])));
+            out.y = int8_pack4(int8_code_i32(d.at<E>(f[4])), int8_code_i32(d.at<E>(f[5])),
+                               int8_code_i32(d.at<E>(f[6])), int8_code_i32(d.at<E>(f[7])));
         }
     });
     return out;
