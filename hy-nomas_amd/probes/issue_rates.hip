@@ -43,6 +43,11 @@
 //                   16 slots before; the write slots issue fp16 MFMAs into
 //                   four rotating O blocks and their max3 reads the S block
 //                   the step-A chain before them has just produced.
+//   op K           8 independent VALU instructions of one kind per slot, no
+//                  MFMA (K: v_fma_f32, v_mul_f32, v_exp_f32, v_cvt_pk_bf16_f32,
+//                  v_cvt_scalef32_pk_f32_fp8, v_cvt_pk_f16_f32, v_pk_fma_f16,
+//                  v_max3_f32): each kind's own issue cost, in ns per
+//                  instruction per SIMD.
 //   tile+barrier, rotated
 //                   the same, with the waves of the workgroup's upper half
 //                   (the second wave of each SIMD) starting 8 slots later in
@@ -73,7 +78,45 @@ constexpr int SLOTS = 32;  // slots per loop iteration (one attention tile per w
 constexpr int LDS_BYTES = 96 * 1024;
 
 enum Pattern { MFMA = 0, VALU = 1, MFMA_VALU = 2, SPLIT = 3, TILE = 4, TILE_BAR = 5, TILE_BAR_ROT = 6, TILE_BAR_VT = 7, CLUMP_VALU_END = 8, CLUMP_VALU_SPREAD = 9, CLUMP_SALU_END = 10,
-               CLUMP_SALU_SPREAD = 11, CHAIN = 12, TILE_DEP = 13 };
+               CLUMP_SALU_SPREAD = 11, CHAIN = 12, TILE_DEP = 13, VALU_OP = 14 };
+
+// One instruction of VALU kind K on chain x (the VALU_OP pattern).
+constexpr const char* OP_NAMES[8] = {"v_fma_f32", "v_mul_f32", "v_exp_f32", "v_cvt_pk_bf16_f32",
+                                     "v_cvt_scalef32_pk_f32_fp8", "v_cvt_pk_f16_f32", "v_pk_fma_f16", "v_max3_f32"};
+template <int K>
+__device__ __forceinline__ void kind_op(float& x, float c) {
+    if (K == 0) asm volatile("v_fma_f32 %0, %0, %1, 0.5" : "+v"(x) : "v"(c));
+    if (K == 1) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(c));
+    if (K == 2) asm volatile("v_exp_f32 %0, %0" : "+v"(x));
+    if (K == 3) asm volatile("v_cvt_pk_bf16_f32 %0, %0, %1" : "+v"(x) : "v"(c));
+    if (K == 4) {
+        double d;
+        asm volatile("v_cvt_scalef32_pk_f32_fp8 %0, %1, 1.0" : "=v"(d) : "v"(x));
+        x = __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint64_t, d));
+    }
+    if (K == 5) asm volatile("v_cvt_pk_f16_f32 %0, %0, %1" : "+v"(x) : "v"(c));
+    if (K == 6) asm volatile("v_pk_fma_f16 %0, %0, %1, %0" : "+v"(x) : "v"(c));
+    if (K == 7) asm volatile("v_max3_f32 %0, %0, %1, 0.5" : "+v"(x) : "v"(c));
+}
+
+// 8 chains of VALU kind K per slot, no MFMA.
+template <int K>
+__device__ __forceinline__ float op_loop(int iters) {
+    float x[8];
+    for (int i = 0; i < 8; ++i) x[i] = 0.01f * (threadIdx.x + i);
+    const float c = 0.999f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) kind_op<K>(x[j], c);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < 8; ++i) sum += x[i];
+    return sum;
+}
 
 __device__ __forceinline__ void fma_op(float& x, float c) { asm volatile("v_fma_f32 %0, %0, %1, 0.5" : "+v"(x) : "v"(c)); }
 
@@ -280,6 +323,7 @@ __global__ void issue_kernel(int iters, float* out) {
     else if (PAT == TILE_BAR_VT) sum = slot_loop<true, 2, 0, true, false, true>(iters, lds);
     else if (PAT == CHAIN) sum = chain_loop(iters);
     else if (PAT == TILE_DEP) sum = dep_loop<true>(iters, lds);
+    else if (PAT == VALU_OP) sum = op_loop<NV>(iters);
     else if (PAT == CLUMP_VALU_END) sum = slot_loop<true, 2, 0, true, false, false, 1, false>(iters, lds);
     else if (PAT == CLUMP_VALU_SPREAD) sum = slot_loop<true, 2, 0, true, false, false, 1, true>(iters, lds);
     else if (PAT == CLUMP_SALU_END) sum = slot_loop<true, 2, 0, true, false, false, 2, false>(iters, lds);
@@ -346,6 +390,21 @@ int main() {
         line("tile + barrier + 16 SALU at tile end", run<CLUMP_SALU_END, 0>(threads, out), true);
         line("tile + barrier + 16 SALU, 1 per slot", run<CLUMP_SALU_SPREAD, 0>(threads, out), true);
     }
+    // Per-instruction cost of each VALU kind: slot time / 8.
+    printf("\n%-28s %14s %14s %14s\n", "VALU kind (ns per instr)", "1 w/SIMD", "2 w/SIMD", "3 w/SIMD");
+    auto op_row = [&](int k, double (*f)(int, float*)) {
+        printf("%-28s", OP_NAMES[k]);
+        for (int threads : {256, 512, 768}) printf(" %14.3f", f(threads, out) / 8.0);
+        printf("\n");
+    };
+    op_row(0, run<VALU_OP, 0>);
+    op_row(1, run<VALU_OP, 1>);
+    op_row(2, run<VALU_OP, 2>);
+    op_row(3, run<VALU_OP, 3>);
+    op_row(4, run<VALU_OP, 4>);
+    op_row(5, run<VALU_OP, 5>);
+    op_row(6, run<VALU_OP, 6>);
+    op_row(7, run<VALU_OP, 7>);
     CHECK(hipFree(out));
     return 0;
 }
