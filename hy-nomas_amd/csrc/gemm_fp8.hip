@@ -315,16 +315,13 @@ HN_DEVICE void mfma_slice_partial(f32x16 (&acc)[4][4], const Frags& f, int imax,
             if (i < imax && j < jmax) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
 }
 
-// Work item (XCD x = id % 8, position i = id / 8 in that XCD's queue) -> tile.
-// An XCD's queue holds its share of the full tiles, in groups of GROUP_M tile
-// rows walking N (so the ~32 tiles it runs at once share A and B panels in its
-// L2), followed by its share of the edge tiles. Edge tiles skip the MFMAs of
-// blocks outside the matrix and so run shorter; queued last, they fill the
-// final round instead of adding one: at the north-star shape (43 x 48 tiles,
-// the last tile row 48 rows deep) each XCD gets 252 full and 6 half-length
-// tiles -- eight rounds of its 32 CUs instead of nine.
-HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) {
-    const int x = id & 7, i = id >> 3;
+// Queue entry i of XCD x -> tile. An XCD's queue holds its share of the full
+// tiles, in groups of GROUP_M tile rows walking N (so the ~32 tiles it runs at
+// once share A and B panels in its L2), followed by its share of the edge
+// tiles. Edge tiles skip the MFMAs of blocks outside the matrix and run
+// shorter (a 48-row edge tile about 0.45-0.65 of a full one: their DMAs,
+// barriers and epilogue stay).
+HN_DEVICE bool tile_at(const Params& p, int x, int i, int& tm, int& tn) {
     const int F = p.tiles_full, P = p.tiles_part;
     const int fx = F / 8 + (x < F % 8 ? 1 : 0);
     if (i < fx) {
@@ -346,6 +343,36 @@ HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) {
     tm = g;
     tn = p.tn_full;
     return true;
+}
+
+// One workgroup per queue entry (id = x + 8 i).
+HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) { return tile_at(p, id & 7, id >> 3, tm, tn); }
+
+// Persistent launches: workgroup s of XCD x's S runs the queue's full tiles
+// s, s + S, s + 2 S, ... (round k: entry k S + s). Of the fx full tiles, the
+// first r = fx % S workgroups ("heavy") get one more than the other L = S - r
+// ("light"). The edge tiles go to the light workgroups only, dealt round-robin
+// after their full tiles, whenever there are at most 2 L of them: a light
+// workgroup then ends at most two edge tiles (about one full tile) after its
+// last full one, where dealing them on round-robin across all workgroups
+// would give heavy ones an edge tile on top of their extra full one.
+// Measured against the plain order (same box): 10 800 x 3072 x 12 288 (43 x
+// 12 tiles, 63 full and 1.5 edge tiles per XCD) 361.6 -> 347.5 us, the north
+// star (252 full and 6 edge tiles per XCD, S = 32) 381 -> 378 us, which is
+// still 4 % above 10 752 rows (no edge tiles): two 48-row edge tiles take
+// longer than a full one. With more than 2 L edge tiles, they follow the
+// plain round-robin order.
+HN_DEVICE bool tile_of_slot(const Params& p, int x, int i, int S, int& tm, int& tn) {
+    const int F = p.tiles_full, P = p.tiles_part;
+    const int fx = F / 8 + (x < F % 8 ? 1 : 0);
+    const int px = P / 8 + (x < P % 8 ? 1 : 0);
+    const int r = fx % S, L = r ? S - r : S;
+    if (i < fx || px > 2 * L) return tile_at(p, x, i, tm, tn);
+    const int s = i % S, k = i / S;
+    if (s < r) return false;                   // heavy: no edge tiles
+    const int q = (k - fx / S) * L + (s - r);  // this light workgroup's edge tile
+    if (q >= px) return false;
+    return tile_at(p, x, fx + q, tm, tn);
 }
 
 // ---------------------------------------------------------------------------
@@ -965,7 +992,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     const int stride = (int)(gridDim.x >> 3);  // workgroups per XCD
     int slot = (int)(blockIdx.x >> 3);
     int tm, tn;
-    if (!tile_of(p, xcd + 8 * slot, tm, tn)) return;
+    if (!tile_of_slot(p, xcd, slot, stride, tm, tn)) return;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1163,7 +1190,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 
     for (;;) {
         int ntm = 0, ntn = 0;
-        const bool more = tile_of(p, xcd + 8 * (slot + stride), ntm, ntn);
+        const bool more = tile_of_slot(p, xcd, slot + stride, stride, ntm, ntn);
         // Slice (0, 0).
         {
             const uint8_t* const ab = smem + (2 * pair_of(0)) * R_BUF;
