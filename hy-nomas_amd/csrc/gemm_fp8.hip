@@ -33,7 +33,6 @@ namespace gemm {
 
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int NT = 256;
-constexpr int GROUP_M = 8;
 constexpr int TILE_BYTES = BM * BK;         // one operand tile, 32 KB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;  // A + B
 
@@ -315,65 +314,8 @@ HN_DEVICE void mfma_slice_partial(f32x16 (&acc)[4][4], const Frags& f, int imax,
             if (i < imax && j < jmax) acc[i][j] = mfma(f.b[i], f.a[j], acc[i][j]);
 }
 
-// Queue entry i of XCD x -> tile. An XCD's queue holds its share of the full
-// tiles, in groups of GROUP_M tile rows walking N (so the ~32 tiles it runs at
-// once share A and B panels in its L2), followed by its share of the edge
-// tiles. Edge tiles skip the MFMAs of blocks outside the matrix and run
-// shorter (a 48-row edge tile about 0.45-0.65 of a full one: their DMAs,
-// barriers and epilogue stay).
-HN_DEVICE bool tile_at(const Params& p, int x, int i, int& tm, int& tn) {
-    const int F = p.tiles_full, P = p.tiles_part;
-    const int fx = F / 8 + (x < F % 8 ? 1 : 0);
-    if (i < fx) {
-        const int f = x * (F / 8) + min(x, F % 8) + i;
-        const int per_group = GROUP_M * p.tn_full;
-        const int first_m = (f / per_group) * GROUP_M;
-        const int gm = min(GROUP_M, p.tm_full - first_m);
-        tm = first_m + (f % per_group) % gm;
-        tn = (f % per_group) / gm;
-        return true;
-    }
-    const int q = i - fx;
-    if (q >= P / 8 + (x < P % 8 ? 1 : 0)) return false;
-    int g = x * (P / 8) + min(x, P % 8) + q;
-    if (p.m_tail) {
-        if (g < p.tiles_n) { tm = p.tm_full; tn = g; return true; }
-        g -= p.tiles_n;
-    }
-    tm = g;
-    tn = p.tn_full;
-    return true;
-}
-
 // One workgroup per queue entry (id = x + 8 i).
 HN_DEVICE bool tile_of(const Params& p, int id, int& tm, int& tn) { return tile_at(p, id & 7, id >> 3, tm, tn); }
-
-// Persistent launches: workgroup s of XCD x's S runs the queue's full tiles
-// s, s + S, s + 2 S, ... (round k: entry k S + s). Of the fx full tiles, the
-// first r = fx % S workgroups ("heavy") get one more than the other L = S - r
-// ("light"). The edge tiles go to the light workgroups only, dealt round-robin
-// after their full tiles, whenever there are at most 2 L of them: a light
-// workgroup then ends at most two edge tiles (about one full tile) after its
-// last full one, where dealing them on round-robin across all workgroups
-// would give heavy ones an edge tile on top of their extra full one.
-// Measured against the plain order (same box): 10 800 x 3072 x 12 288 (43 x
-// 12 tiles, 63 full and 1.5 edge tiles per XCD) 361.6 -> 347.5 us, the north
-// star (252 full and 6 edge tiles per XCD, S = 32) 381 -> 378 us, which is
-// still 4 % above 10 752 rows (no edge tiles): two 48-row edge tiles take
-// longer than a full one. With more than 2 L edge tiles, they follow the
-// plain round-robin order.
-HN_DEVICE bool tile_of_slot(const Params& p, int x, int i, int S, int& tm, int& tn) {
-    const int F = p.tiles_full, P = p.tiles_part;
-    const int fx = F / 8 + (x < F % 8 ? 1 : 0);
-    const int px = P / 8 + (x < P % 8 ? 1 : 0);
-    const int r = fx % S, L = r ? S - r : S;
-    if (i < fx || px > 2 * L) return tile_at(p, x, i, tm, tn);
-    const int s = i % S, k = i / S;
-    if (s < r) return false;                   // heavy: no edge tiles
-    const int q = (k - fx / S) * L + (s - r);  // this light workgroup's edge tile
-    if (q >= px) return false;
-    return tile_at(p, x, fx + q, tm, tn);
-}
 
 // ---------------------------------------------------------------------------
 // Blockwise-scaled kernel, 8 waves: a 512-thread workgroup owns a 256 x 256
@@ -1290,15 +1232,12 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     const int64_t tm = (M + gemm::BM - 1) / gemm::BM;
     HN_REQUIRE(tm * ((N + 191) / 192) <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
     auto set_tiles = [&](int bn) {
-        const int64_t tn = (N + bn - 1) / bn;
+        const gemm::TileCounts t = gemm::tile_counts(M, N, bn);
         p.bn = bn;
-        p.tiles_m = (int)tm; p.tiles_n = (int)tn;
-        p.tm_full = (int)(M / gemm::BM);
-        p.tn_full = (int)(N / bn);
-        p.m_tail = (int)(M % gemm::BM != 0);
-        p.tiles_full = p.tm_full * p.tn_full;
-        p.tiles_part = (int)(tm * tn) - p.tiles_full;
-        p.per_xcd = mode == gemm::ROWCOL ? (p.tiles_full + 7) / 8 + (p.tiles_part + 7) / 8 : (int)((tm * tn + 7) / 8);
+        p.tiles_m = t.tiles_m; p.tiles_n = t.tiles_n;
+        p.tm_full = t.tm_full; p.tn_full = t.tn_full; p.m_tail = t.m_tail;
+        p.tiles_full = t.tiles_full; p.tiles_part = t.tiles_part;
+        p.per_xcd = mode == gemm::ROWCOL ? t.per_xcd : (int)((tm * t.tiles_n + 7) / 8);
     };
     set_tiles(gemm::BN);
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
