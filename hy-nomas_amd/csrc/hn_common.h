@@ -121,9 +121,12 @@ struct Quot {
 // ceil(v - 0.5) (each add rounded in fp32), then clamp to +-127. Round to
 // nearest is symmetric, so v - 0.5 rounds to -(|v| + 0.5) rounded and
 // ceil(v - 0.5) = -floor(|v| + 0.5): the code is sign(v) min(floor(|v| + 0.5),
-// 127) for either sign (-0 and +0 both give 0).
+// 127) for either sign (-0 and +0 both give 0). With t = min(|v| + 0.5, 127)
+// >= 0, floor(t) = trunc(t) and min(floor(x), 127) = floor(min(x, 127)) (127
+// is an integer), so the float-to-int conversion's truncation toward zero of
+// copysign(t, v) is the code: no floor instruction.
 HN_DEVICE int int8_code_i32(float v) {
-    const float t = fminf(floorf(fabsf(v) + 0.5f), 127.0f);
+    const float t = fminf(fabsf(v) + 0.5f, 127.0f);
     return (int)__builtin_copysignf(t, v);
 }
 
