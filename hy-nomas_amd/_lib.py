@@ -54,6 +54,7 @@ SIGNATURES = {
     "hn_attn_fp8kv_noalloc_scratch_bytes": [],
     "hn_qk_norm_rope_kv": [_I, _P, _P, _P, _PI64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _F,
                            _P, _P, _PI64, _P, _P, _PI64, _I64, _I64, _P, _P],
+    "hn_e4m3_encode_range": [ctypes.c_uint32, _I64, _P, _P],
 }
 RESTYPES = {"hn_last_error": ctypes.c_char_p, "hn_attn_fp8kv_workspace_size": _I64,
             "hn_attn_fp8kv_noalloc_scratch_bytes": _I64}

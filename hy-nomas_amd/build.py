@@ -61,25 +61,5 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
-PROBES = PKG / "probes"
-
-
-def build_probes(verbose: bool = False) -> list[Path]:
-    """Compile the standalone measurement programs under probes/ (each
-    <name>.hip -> an executable <name> beside it)."""
-    built = []
-    for src in sorted(PROBES.glob("*.hip")):
-        exe = src.with_suffix("")
-        cmd = [HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], str(src), "-o", str(exe)]
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
-        built.append(exe)
-    if verbose:
-        print(f"built {len(built)} probe(s) under {PROBES}", file=sys.stderr)
-    return built
-
-
 if __name__ == "__main__":
     build(verbose=True)
-    build_probes(verbose=True)

@@ -703,3 +703,30 @@ extern "C" int hn_kv_dequantize(int fmt, const void* q, const int64_t* qs, const
         kv_dequantize_kernel<HN_KV_INT8><<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(a);
     return check_launch("hn_kv_dequantize");
 }
+
+// Encodes the fp32 values with bit patterns first, first + 1, ... with the
+// quantizers' own conversion (e4m3_encode4), four per thread in one word.
+__global__ __launch_bounds__(256) void e4m3_encode_range_kernel(uint32_t first, int64_t words,
+                                                                uint32_t* out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words; w += stride) {
+        const uint32_t b = first + (uint32_t)(w * 4);
+        out[w] = e4m3_encode4(__uint_as_float(b), __uint_as_float(b + 1u), __uint_as_float(b + 2u),
+                              __uint_as_float(b + 3u));
+    }
+}
+
+extern "C" int hn_e4m3_encode_range(uint32_t first, int64_t n, void* out, void* stream) {
+    HN_REQUIRE(n >= 0 && n % 4 == 0, HN_E_ARG, "hn_e4m3_encode_range: n must be a multiple of 4");
+    HN_REQUIRE((uint64_t)first + (uint64_t)n <= (1ull << 32), HN_E_ARG,
+               "hn_e4m3_encode_range: the range passes the last fp32 bit pattern");
+    HN_REQUIRE(aligned(out, 4), HN_E_ARG, "hn_e4m3_encode_range: out must be 4-byte aligned");
+    if (n == 0) return HN_OK;
+    HN_REQUIRE(out, HN_E_ARG, "hn_e4m3_encode_range: null output");
+    if (const int rc = require_gfx950("hn_e4m3_encode_range"); rc != HN_OK) return rc;
+    const int64_t words = n / 4;
+    const int64_t grid = stream_grid((words + 255) / 256, 8);
+    e4m3_encode_range_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(first, words,
+                                                                              (uint32_t*)out);
+    return check_launch("hn_e4m3_encode_range");
+}

@@ -249,6 +249,14 @@ int hn_qk_norm_rope_kv(int fmt, void *q, void *k, const void *v, const int64_t *
                        const int64_t *ss, int64_t cap, int64_t start, int32_t *status,
                        void *stream);
 
+/* Test support; it replaces no reference interface. Writes to out[i] the e4m3
+ * byte that the quantizers' hardware conversion (v_cvt_pk_fp8_f32, round to
+ * nearest even) gives for the fp32 value whose bit pattern is first + i, for
+ * i in [0, n). n must be a multiple of 4 and first + n <= 2^32. Exists so
+ * that tests can compare that conversion, over every input the quantizers can
+ * produce (|x| <= 448.5), with the CPU oracle's encoder. */
+int hn_e4m3_encode_range(uint32_t first, int64_t n, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -87,6 +87,28 @@ void hn_oracle_e4m3_decode_n(const uint8_t *q, int64_t n, float *y)
         y[i] = hn_oracle_e4m3_decode(q[i]);
 }
 
+/* codes[i] against hn_oracle_e4m3_encode of the fp32 value whose bit pattern is
+ * first + i, for i in [0, n): returns how many differ; *first_bad gets the
+ * first differing index (-1 when none). Used to check a device conversion over
+ * whole ranges of fp32 bit patterns. */
+int64_t hn_oracle_e4m3_range_mismatches(uint32_t first, int64_t n, const uint8_t *codes,
+                                        int64_t *first_bad)
+{
+    int64_t bad = 0;
+    *first_bad = -1;
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t b = first + (uint32_t)i;
+        float f;
+        memcpy(&f, &b, sizeof f);
+        if (hn_oracle_e4m3_encode(f) != codes[i]) {
+            if (bad == 0)
+                *first_bad = i;
+            ++bad;
+        }
+    }
+    return bad;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Scale rules.
  *  mode 0 ("clamp"):  s = max(amax, floor) / 448

@@ -67,6 +67,8 @@ def lib():
         L.hn_oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
         L.hn_oracle_e4m3_encode_f32.argtypes = [P, I64, P]
         L.hn_oracle_e4m3_decode_n.argtypes = [P, I64, P]
+        L.hn_oracle_e4m3_range_mismatches.restype = I64
+        L.hn_oracle_e4m3_range_mismatches.argtypes = [ctypes.c_uint32, I64, P, P]
         L.hn_oracle_quantize_rows_fp8.argtypes = [P, I64, I64, I64, ctypes.c_int,
                                                   ctypes.c_float, P, P]
         L.hn_oracle_quantize_blockwise_fp8.argtypes = [P, I64, I64, P, P]
@@ -103,6 +105,15 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.shape, dtype=np.uint8)
     lib().hn_oracle_e4m3_encode_f32(_ptr(x), x.size, _ptr(out))
     return out
+
+
+def e4m3_range_mismatches(first: int, codes: np.ndarray):
+    """(count, first index) of codes[i] != e4m3 encode of the fp32 bit pattern
+    first + i (first index -1 when every code agrees)."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    where = ctypes.c_int64(-1)
+    bad = lib().hn_oracle_e4m3_range_mismatches(first, codes.size, _ptr(codes), ctypes.byref(where))
+    return int(bad), int(where.value)
 
 
 def e4m3_decode(q: np.ndarray) -> np.ndarray:

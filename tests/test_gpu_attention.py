@@ -575,3 +575,97 @@ def test_installed_seam_fallback_rules(dev):
                                               None, None, 0, "magi", dense)
     assert f8["dense_layer_stats"] == {"denoise": 1, "write": 0}
     hook.uninstall()
+
+
+def test_installed_seam_torch_mode_keeps_padded_query_rows(O, dev):
+    """attn_mode "torch": the reference's SDPA branch (nomas_cpt.py:771-781)
+    passes kv_mask as the attention mask for quantized storage and does not
+    zero padded query rows, so a padded text query keeps its attention over
+    the valid keys."""
+    ca = pkg_module("cache_attention")
+    kvc = pkg_module("fp8_kv_cache")
+    native, calls = _stand_in_native()
+    hook = ca.FP8CacheAttention(native)
+    H, D, Li, Lt = 2, 128, 80, 24
+    cache = _cache_from_chunks(dev, 2, 100, H, D, seed=41, capacity=600)
+    valid = 200
+    cmask = torch.ones(1, 600, dtype=torch.bool, device=dev)
+    cmask[0, 130:150] = False
+    g = torch.Generator(device=dev).manual_seed(42)
+
+    def rnd(B, L):
+        return torch.randn(B, L, H, D, device=dev, generator=g).to(torch.bfloat16)
+
+    tm = torch.ones(1, Lt, dtype=torch.bool, device=dev)
+    tm[0, 15:] = False
+    for update, cache_txt in ((False, True), (True, False)):
+        q, k, v = (rnd(1, Li), rnd(1, Lt)), (rnd(1, Li), rnd(1, Lt)), (rnd(1, Li), rnd(1, Lt))
+        ref = _reference_cached_attention(O, q, k, v, _dequant(O, cache, valid),
+                                          cmask[0, :valid].cpu().numpy(), tm, update, cache_txt, True,
+                                          attn_mode="torch")
+        with torch.no_grad():
+            img, txt = native.causal_attention_with_cache_mp(q, k, v, cache, valid, "torch", tm, update,
+                                                             cache_txt, cmask)
+        got = torch.cat([img[0], txt[0]], 0).float().cpu().numpy().reshape(Li + Lt, H, D)
+        assert_close_bf16(got, ref[0], what=f"torch mode update={update}")
+        assert (txt[0].reshape(Lt, H, D)[15:].abs().sum() > 0), "padded rows keep SDPA's values"
+        if update:
+            valid += Li
+    assert not calls
+    hook.uninstall()
+
+
+def test_pipeline_fp8_storage_write_and_audit(O, dev):
+    """The stand-in AR pipeline (tests/standin_pipeline.py) with the FP8
+    storage binding and the attention seam installed: it selects
+    kv_cache_quantization fp8, allocates FP8 blocks on the GPU, writes a
+    chunk through an update pass (codes and scales bit-exact), grows its
+    capacity, and audits its caches with the keys causal_ar.py:3365-3374
+    reads."""
+    from standin_pipeline import args_for, make_reference
+    st = pkg_module("kv_cache_storage")
+    ca = pkg_module("cache_attention")
+    storage, int8_kv, Pipeline = make_reference()
+    native, calls = _stand_in_native()
+    store_hook = st.install_fp8_kv_storage(storage, pipeline_cls=Pipeline, int8_kv_module=int8_kv)
+    attn_hook = ca.FP8CacheAttention(native)
+    try:
+        H, D, Li, Lt = 2, 128, 96, 32
+        pipe = Pipeline(args_for("fp8"), hidden_size=H * D, heads_num=H, num_double_blocks=2)
+        pipe._initialize_kv_cache(1, Li + Lt, torch.bfloat16, dev)
+        g = torch.Generator(device=dev).manual_seed(5)
+
+        def rnd(L, s):
+            return (torch.randn(1, L, H, D, device=dev, generator=g) * s).to(torch.bfloat16)
+
+        tm = torch.ones(1, Lt, dtype=torch.bool, device=dev)
+        tm[0, 28:] = False
+        for layer, cache in enumerate(pipe.kv_cache):
+            q, k, v = (rnd(Li, 1), rnd(Lt, 1)), (rnd(Li, 2), rnd(Lt, 2)), (rnd(Li, 3), rnd(Lt, 3))
+            with torch.no_grad():
+                native.causal_attention_with_cache_mp(q, k, v, cache, pipe.cache_valid_len, "flash3", tm,
+                                                      True, True, pipe.cache_mask_list[layer])
+            for name, cur in (("k", k), ("v", v)):
+                x = torch.cat(cur, 1)
+                qo, so = O.kv_quantize(bf16_bits(x))
+                assert np.array_equal(u8(cache[name][:, :Li + Lt]), qo), f"layer {layer} {name} codes"
+                assert np.array_equal(cache[name + "_scale"][:, :Li + Lt].cpu().numpy().view(np.uint32),
+                                      so.view(np.uint32)), f"layer {layer} {name} scales"
+            want = np.concatenate([np.ones(Li, bool), tm[0].cpu().numpy()])
+            assert np.array_equal(pipe.cache_mask_list[layer][0].cpu().numpy(), want)
+        pipe.cache_valid_len += Li + Lt
+        before = [u8(c["k"]).copy() for c in pipe.kv_cache]
+        pipe._ensure_kv_cache_capacity(400)
+        for c, b in zip(pipe.kv_cache, before):
+            assert c["k"].dtype == torch.float8_e4m3fn and c["k"].shape[1] == 400
+            assert np.array_equal(u8(c["k"][:, :Li + Lt]), b)
+        audit = pipe.storage_audit()
+        assert audit["kv_storage_format"] == "fp8" and audit["int8_kv"] is False
+        per_layer = 2 * 400 * H * D + 2 * 400 * H * 4
+        assert audit["gpu_kv_storage_bytes"] == 2 * per_layer
+        assert audit["gpu_kv_peak_working_bytes_upper_bound"] == 2 * per_layer
+        assert audit["codec_stats"] == [{}, {}]
+        assert not calls and attn_hook.stats["calls"] == 2
+    finally:
+        attn_hook.uninstall()
+        store_hook.uninstall()

@@ -65,6 +65,14 @@ def _edge_rows(cols):
     r = (rng.integers(0, 0x7F7F, cols) | (rng.integers(0, 2, cols) << 15)).astype(np.uint16)
     r[0] = 0x7F7F                                             # bf16 max with every magnitude below it
     rows.append(r)
+    # peak 127: the INT8 scale is exactly 1, so x / s sits on the half-away
+    # ties and on the +-127 clamp (int8_kv_cache.py:150-157); -0 keeps code 0
+    ties = np.array([0.5, 1.5, 2.5, 3.5, 63.5, 125.5, 126.5, 127.0, 126.0, 0.25, 0.75, 1.0],
+                    np.float32)
+    vals = np.concatenate([ties, -ties, [-0.0, 0.0]]).astype(np.float32)
+    r = (rng.integers(0, 0x42FE, cols) | (rng.integers(0, 2, cols) << 15)).astype(np.uint16)
+    r[:vals.size] = (vals.view(np.uint32) >> 16).astype(np.uint16)
+    rows.append(r)
     return np.stack(rows)
 
 
@@ -304,3 +312,40 @@ def test_quantizers_non_finite_rows(O, dev, cols):
         assert np.isnan(so[[3, 7, 11, 15]]).all()
         assert np.array_equal(s.cpu().numpy(), so, equal_nan=True)
         assert _codes_match(u8(q), qo)
+
+
+def test_hardware_e4m3_conversion_matches_oracle_over_quantizer_range(O, dev):
+    """The quantizers encode with gfx950's v_cvt_pk_fp8_f32 (e4m3_encode4 in
+    csrc/hn_common.h). Every quotient they produce is finite with
+    |x / s| <= 448 (1 + 2^-23) < 448.5, so the conversion is checked against
+    the oracle's RNE encoder over every fp32 bit pattern with |x| <= 448.5,
+    both signs (2 x 1.14e9 inputs): no code may differ."""
+    from concurrent.futures import ThreadPoolExecutor
+    L = pkg_module("_lib")
+    lib = L.load()
+    last = 0x43E04000                       # 448.5
+    assert np.array([last], np.uint32).view(np.float32)[0] == 448.5
+    chunk = 1 << 27
+    buf = torch.empty(chunk, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    pool = ThreadPoolExecutor(8)            # the oracle call releases the GIL
+    checked = 0
+    for sign in (0, 0x80000000):
+        start = 0
+        while start <= last:
+            n = min(chunk, (last + 1 - start + 3) // 4 * 4)
+            L.check(lib.hn_e4m3_encode_range(sign | start, n, buf.data_ptr(), stream),
+                    "hn_e4m3_encode_range")
+            codes = buf[:n].cpu().numpy()
+            cuts = [n * i // 8 for i in range(9)]
+            jobs = [pool.submit(O.e4m3_range_mismatches, sign | (start + lo), codes[lo:hi])
+                    for lo, hi in zip(cuts, cuts[1:])]
+            for lo, j in zip(cuts, jobs):
+                bad, where = j.result()
+                assert bad == 0, (f"{bad} codes differ from the oracle; first at fp32 bits "
+                                  f"{sign | (start + lo + where):#010x}")
+            checked += n
+            start += n
+    pool.shutdown()
+    print(f"[e4m3] {checked} fp32 inputs, hardware conversion == oracle", flush=True)
+    assert checked >= 2 * (last + 1)
