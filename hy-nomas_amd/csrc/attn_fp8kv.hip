@@ -686,16 +686,33 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     float* const sbuf = reinterpret_cast<float*>(smem + NS * STAGE);  // [2][128]
 
     // XCD-aware work order: workgroup ids are dealt round-robin to the 8 XCDs,
-    // so id % 8 picks a contiguous range of work items -- the query tiles of
-    // the same few heads share that XCD's L2 while they stream its K/V.
+    // so id % 8 picks a contiguous range of work items.
+    //  * No key split: items run (b, h, query tile) with the tile fastest, so
+    //    the query tiles of the same few heads share an XCD's L2 while they
+    //    stream those heads' K/V.
+    //  * Key splits: items run (b, query tile, split, h) with the head
+    //    fastest, so an XCD holds whole key ranges of every head. A token's
+    //    per-head scales are adjacent ([B, cap, H, 1]): the heads of one key
+    //    range then share each scale sector in one L2, where a head-major
+    //    order had every XCD fetch every sector for its few heads.
     const int id = blockIdx.x;
     const int w = (id & 7) * p.per_xcd + (id >> 3);
     if (w >= p.work) return;
-    const int split = w % p.splits;
-    const int wq = w / p.splits;
-    const int qt = wq % p.q_tiles;
-    const int64_t h = (wq / p.q_tiles) % p.H;
-    const int64_t b = wq / (p.q_tiles * (int)p.H);
+    int split, qt;
+    int64_t h, b;
+    if (p.splits > 1) {
+        h = w % p.H;
+        const int ws = w / (int)p.H;
+        split = ws % p.splits;
+        const int wt = ws / p.splits;
+        qt = wt % p.q_tiles;
+        b = wt / p.q_tiles;
+    } else {
+        split = 0;
+        qt = w % p.q_tiles;
+        h = (w / p.q_tiles) % p.H;
+        b = w / (p.q_tiles * (int)p.H);
+    }
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
