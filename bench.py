@@ -45,6 +45,7 @@ C1_M, C1_K, C1_N = 4096, 3072, 3072
 KV_H, KV_L, KV_D = 24, 10800, 128
 ATT_CHUNKS = 8
 ATT_LQ, ATT_LK = KV_L, ATT_CHUNKS * KV_L   # config 3: 10800 queries over 86400 cached keys
+TEXT_TOKENS, TEXT_PAD = 256, 56              # text stream of the config-4 block's extra line
 
 
 def gemm_flops(m, k, n):
@@ -266,9 +267,24 @@ def main():
             "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
             "traffic": gemm_traffic_bytes(),
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over this GEMM "
-                              "(profiles/fp8_gemm_north_star_traffic.json), scaled by the same counters "
-                              "over a 1 GiB copy; not measured inside this run",
+                              "(profiles/hbm_traffic.json: workloads.linear_gemm), scaled by the same "
+                              "counters over a 1 GiB copy; not measured inside this run",
         },
+        # every hot kernel of the step against its own roofline (the GEMM
+        # repeated from `roofline`); attention entries time the whole call
+        # (its launches and the split merge)
+        "rooflines": [
+            roofline_entry("gemm_rowcol_oe_kernel: north-star FP8 GEMM + bias + GELU", "mfma", f_ns,
+                           "flop", ms_gemm, FP8_PEAK_TFLOPS, "TFLOP/s", "linear_gemm"),
+            roofline_entry("kv_quantize_kernel: config-2 K and V write", "hbm", kv_write_bytes(),
+                           "byte", ms_kv, HBM_PEAK_GBS, "GB/s", "kv_write"),
+            roofline_entry("attn_fp8kv_kernel: config-3 chunk attention (bf16 MFMA over e4m3 K/V)",
+                           "mfma", attn_flops(KV_H, KV_L, lk, KV_D), "flop", ms_att, BF16_PEAK_TFLOPS,
+                           "TFLOP/s", "attn_config3"),
+            roofline_entry("attn_fp8kv_kernel + attn_combine_kernel: decode-style attention, "
+                           "Lq 128 over 86 400 cached keys", "hbm", attn_unique_bytes(KV_H, 128, lk, KV_D),
+                           "byte", ms_dec, HBM_PEAK_GBS, "GB/s", "attn_decode"),
+        ],
         "clock_settle": settle,
         "linear": {"ms": round(ms_linear, 4), "tflops": round(linear_tflops, 2),
                    "frac_fp8_peak": round(linear_tflops / FP8_PEAK_TFLOPS, 4),
@@ -436,9 +452,30 @@ def bench_block(args, torch, cache, dev, g, log):
     tflops = (lin + att) / (ms * 1e-3) / 1e12
     stages = {k: round(v["seconds"] * 1e3, 3) for k, v in m.summary().items()}
     log(f"config-4 block {ms:.3f} ms ({tflops:.0f} TFLOP/s); stages (synchronized) ms {stages}")
-    return {"ms": round(ms, 4), "tflops": round(tflops, 2), "linear_tflop": round(lin / 1e12, 4),
-            "attention_tflop": round(att / 1e12, 4), "stage_ms": stages,
-            "shape": {"tokens": KV_L, "hidden": 3072, "heads": KV_H, "cached_tokens": hist}}
+    res = {"ms": round(ms, 4), "tflops": round(tflops, 2), "linear_tflop": round(lin / 1e12, 4),
+           "attention_tflop": round(att / 1e12, 4), "stage_ms": stages,
+           "shape": {"tokens": KV_L, "hidden": 3072, "heads": KV_H, "cached_tokens": hist}}
+    # The same block with the double-stream block's text stream (BASELINE's
+    # config 4 names none): TEXT_TOKENS text tokens, the last TEXT_PAD of them
+    # padding, a segment's first chunk (cache_txt), denoise pass: queries
+    # [img | txt] over [7 cached chunks | img | txt] with the text mask.
+    del blk
+    tblk = db.FP8DiTBlock(3072, KV_H, device=dev, generator=g, text=True)
+    txt = torch.randn(1, TEXT_TOKENS, 3072, device=dev, generator=g).to(torch.bfloat16)
+    vec_txt = torch.randn(1, 3072, device=dev, generator=g).to(torch.bfloat16)
+    tmask = torch.ones(1, TEXT_TOKENS, dtype=torch.bool, device=dev)
+    tmask[0, TEXT_TOKENS - TEXT_PAD:] = False
+    cmask = torch.ones(1, cache["k"].shape[1], dtype=torch.bool, device=dev)
+    tfn = lambda: tblk(img, vec, cos, sin, cache, hist, False, txt=txt, vec_txt=vec_txt,
+                       text_mask=tmask, cache_mask=cmask, cache_txt=True)
+    with torch.no_grad():
+        tms = time_loop(tfn, max(2, args.steps // 4), max(1, args.warmup // 2))
+    tl, ta = block_flops(tokens=KV_L + TEXT_TOKENS, keys=hist + KV_L + TEXT_TOKENS)
+    log(f"config-4 block with {TEXT_TOKENS} text tokens {tms:.3f} ms "
+        f"({(tl + ta) / (tms * 1e-3) / 1e12:.0f} TFLOP/s)")
+    res["with_text"] = {"ms": round(tms, 4), "text_tokens": TEXT_TOKENS, "text_padding": TEXT_PAD,
+                        "tflops": round((tl + ta) / (tms * 1e-3) / 1e12, 2)}
+    return res
 
 
 def ar_chunk_flops(depth=40, prior=16, hidden=3072, heads=24, tokens=KV_L, d=KV_D, passes=5):
@@ -544,16 +581,36 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
             log(f"decode-style attention (Lq=128) {ms * 1e3:.1f} us")
 
 
-def gemm_traffic_bytes():
-    """HBM bytes per north-star GEMM launch from the committed counter summary
-    (profiles/fp8_gemm_north_star_traffic.json), or None."""
-    f = ROOT / "profiles" / "fp8_gemm_north_star_traffic.json"
-    if not f.exists():
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
+
+
+def counter_traffic(workload):
+    """HBM bytes per call of ``workload`` from the committed counter summary
+    (profiles/hbm_traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
+    scaled by the same counters over a plain copy), or None. Not measured in
+    this run: the counters need a rocprofv3 pass of their own."""
+    if not TRAFFIC_FILE.exists():
         return None
     try:
-        return json.loads(f.read_text()).get("hbm_bytes_per_launch")
-    except (ValueError, OSError):
+        entry = json.loads(TRAFFIC_FILE.read_text())["workloads"].get(workload)
+    except (ValueError, OSError, KeyError):
         return None
+    return None if entry is None else entry.get("hbm_bytes_per_call")
+
+
+def gemm_traffic_bytes():
+    """HBM bytes per north-star GEMM launch (profiles/hbm_traffic.json), or None."""
+    return counter_traffic("linear_gemm")
+
+
+def roofline_entry(name, bound, work, unit_work, ms, peak, unit, traffic_key):
+    """One kernel's position against its roofline: ``work`` algorithmic flop
+    or bytes per call over the measured ms per call, against ``peak``."""
+    rate = work / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    return {"kernel": name, "bound": bound, "work_per_call": work, "work_unit": unit_work,
+            "ms_per_call": round(ms, 5), "achieved": round(rate, 2), "peak": peak, "unit": unit,
+            "frac": round(rate / peak, 4), "traffic": counter_traffic(traffic_key),
+            "traffic_source": f"profiles/hbm_traffic.json: workloads.{traffic_key}"}
 
 
 def _median_seconds(fn, reps=5, warmup=2):

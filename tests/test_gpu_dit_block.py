@@ -297,6 +297,161 @@ def test_ar_chunk_loop_structure(dev):
 
 
 # ---------------------------------------------------------------------------
+# The text stream of the double-stream block (nomas_compile_prepost.py:37-38,
+# 55-63, 90-98) and its cached attention over [history | img | txt]
+# (nomas_cpt.py:464-685 with the quantized-storage key and mask table).
+
+def ref_pre_txt(blk, txt, vec_txt):
+    txt, vec = _cpu(txt), _cpu(vec_txt)
+    B, L, C = txt.shape
+    H, D = blk.heads, blk.head_dim
+    parts = F.linear(F.silu(vec), _cpu(blk.txt_mod.weight), _cpu(blk.txt_mod.bias)).chunk(6, dim=-1)
+    x = _modulate(F.layer_norm(txt, (C,), eps=1e-6), parts[0], parts[1])
+    q, k, v = _ref_linear(blk.txt_qkv, x).view(B, L, 3, H, D).unbind(2)
+    q = _rms_norm(q, _cpu(blk.txt_q_norm), 1e-6).to(v)
+    k = _rms_norm(k, _cpu(blk.txt_k_norm), 1e-6).to(v)
+    return q, k, v, parts
+
+
+def ref_post_txt(blk, txt, attn, parts):
+    txt, attn = _cpu(txt), _cpu(attn).to(torch.bfloat16)
+    parts = [_cpu(p) for p in parts]
+    B, L, C = txt.shape
+    txt = txt + _ref_linear(blk.txt_proj, attn.reshape(B, L, C)) * parts[2].unsqueeze(1)
+    h = _modulate(F.layer_norm(txt, (C,), eps=1e-6), parts[3], parts[4])
+    h = _ref_linear(blk.txt_fc2, _ref_linear(blk.txt_fc1, h, gelu=True))
+    return txt + h * parts[5].unsqueeze(1)
+
+
+def ref_attention_two_streams(q, tq, k, tk, v, tv, hist_k, hist_v, hist_valid, text_valid):
+    """fp32 softmax attention of queries [img | txt] over [history | img | txt]
+    with key validity [hist_valid | all | text_valid]; padded text query rows
+    are zero (the flash3/Flex paths' output, nomas_cpt.py:782-829)."""
+    qf = torch.cat([_cpu(q), _cpu(tq)], 1).float()
+    keys = torch.cat([hist_k, _cpu(k).float(), _cpu(tk).float()], 1)
+    vals = torch.cat([hist_v, _cpu(v).float(), _cpu(tv).float()], 1)
+    valid = torch.cat([hist_valid, torch.ones(q.shape[1], dtype=torch.bool), text_valid])
+    out = torch.zeros_like(qf)
+    for h in range(qf.shape[2]):
+        s = qf[0, :, h] @ keys[0, :, h].T / math.sqrt(qf.shape[-1])
+        s[:, ~valid] = -float("inf")
+        out[0, :, h] = torch.softmax(s, dim=-1) @ vals[0, :, h]
+    out[0, q.shape[1]:][~text_valid] = 0.0
+    return out
+
+
+@pytest.mark.parametrize("update_cache", [False, True])
+def test_block_text_stream(dev, update_cache):
+    """Both streams of one block (hidden 512, 4 heads): the text stream's
+    pre-attention, the cached attention of queries [img | txt] over
+    [history (with a hole) | img | txt (padded)], each stream's
+    post-attention, stage by stage on the GPU's own inputs; the block's
+    outputs against the CPU restatement end to end; and on an update pass
+    the cache write of img + txt K/V and the cache mask."""
+    print(f"case dit block text stream update_cache={update_cache}", flush=True)
+    db = pkg_module("dit_block")
+    kvc = pkg_module("fp8_kv_cache")
+    ca = pkg_module("cache_attention")
+    hidden, heads, Lt = 512, 4, 24
+    _, cache, hist, hk, hv, img, vec, cos, sin, L = _setup(dev, hidden, heads)
+    g = torch.Generator(device=dev).manual_seed(17)
+    blk = db.FP8DiTBlock(hidden, heads, device=dev, generator=g, text=True)
+    txt = torch.randn(1, Lt, hidden, device=dev, generator=g).to(torch.bfloat16)
+    vec_txt = torch.randn(1, hidden, device=dev, generator=g).to(torch.bfloat16)
+    text_mask = torch.ones(1, Lt, dtype=torch.bool, device=dev)
+    text_mask[0, Lt - 5:] = False
+    cache_mask = torch.zeros(1, cache["k"].shape[1], dtype=torch.bool, device=dev)
+    cache_mask[0, :hist] = True
+    cache_mask[0, 40:60] = False                     # a hole in the history
+    hist_valid = cache_mask[0, :hist].cpu()
+    tv_cpu = text_mask[0].cpu()
+    with torch.no_grad():
+        q, k, v, parts = blk.pre_attention(img, vec, cos, sin)
+        tq, tk, tv, tparts = blk.pre_attention_txt(txt, vec_txt)
+        rq, rk, rv, rparts = ref_pre_txt(blk, txt, vec_txt)
+        for name, got, want, bf in (("q", tq, rq, True), ("k", tk, rk, True), ("v", tv, rv, False)):
+            assert_close_bf16(_cpu(got).float().numpy(), want.float().numpy(), what=f"text pre {name}",
+                              ref_is_bf16=bf)
+        mask_before = cache_mask.clone()
+        ia, ta = ca.causal_attention_with_cache_mp((q, tq), (k, tk), (v, tv), cache, hist, "flash3",
+                                                   text_mask, update_cache, True, cache_mask)
+        ra = ref_attention_two_streams(q, tq, k, tk, v, tv, hk, hv, hist_valid, tv_cpu)
+        got = torch.cat([_cpu(ia), _cpu(ta)], 1).float().reshape(ra.shape)
+        assert_close_bf16(got.numpy(), ra.numpy(), what="two-stream cached attention")
+        assert (_cpu(ta).reshape(1, Lt, heads, 128)[0, Lt - 5:] == 0).all()
+        if update_cache:
+            want = torch.cat([mask_before[0, :hist].cpu(), torch.ones(L, dtype=torch.bool), tv_cpu])
+            assert torch.equal(cache_mask[0, :hist + L + Lt].cpu(), want)
+            check = kvc.make_fp8_kv_block(1, L + Lt, heads, 128, device=dev)
+            kvc.quantize_kv_pair_into(check, torch.cat([k, tk], 1), torch.cat([v, tv], 1), 0)
+            for key in ("k", "v"):
+                assert torch.equal(cache[key][:, hist:hist + L + Lt].view(torch.uint8),
+                                   check[key].view(torch.uint8)), key
+            cache_mask.copy_(mask_before)
+        tout = blk.post_attention_txt(txt, ta, tparts)
+        rto = ref_post_txt(blk, txt, ta, tparts)
+        assert_close_bf16(_cpu(tout).float().numpy(), rto.float().numpy(), what="text post-attention")
+        # the whole block (its own cache write on update passes: restore first)
+        if update_cache:
+            for buf in cache.values():
+                buf[:, hist:].view(torch.uint8).zero_()
+        out_img, out_txt = blk(img, vec, cos, sin, cache, hist, update_cache, txt=txt, vec_txt=vec_txt,
+                               text_mask=text_mask, cache_mask=cache_mask, cache_txt=True)
+    rq_i, rk_i, rv_i, rparts_i = ref_pre(blk, img, vec, cos, sin)
+    ra_all = ref_attention_two_streams(rq_i, rq, rk_i, rk, rv_i, rv, hk, hv, hist_valid, tv_cpu)
+    ro_img = ref_post(blk, img, ra_all[:, :L], rparts_i)
+    ro_txt = ref_post_txt(blk, txt, ra_all[:, L:], rparts)
+    for name, gotv, want in (("img", out_img, ro_img), ("txt", out_txt, ro_txt)):
+        rel = _rel(_cpu(gotv).float(), want.float())
+        print(f"text block {name} output rel-L2 {rel:.3e}", flush=True)
+        assert torch.isfinite(_cpu(gotv)).all() and rel <= OUTPUT_REL_L2
+
+
+def test_ar_chunk_loop_with_text(dev):
+    """A 2-block model with the text stream over two chunks: every write pass
+    stores img + txt K/V, the cache masks hold the padded text keys invalid,
+    the valid length advances by image + text tokens, the second chunk
+    attends the first, and reruns are bit-identical."""
+    print("case ar chunk loop with text", flush=True)
+    db = pkg_module("dit_block")
+    Lt = 12
+    kw = dict(depth=2, hidden=256, heads=2, latent_shape=(1, 4, 5), max_chunks=3, device=dev, text_len=Lt)
+    m1, m2 = db.FP8ARModel(seed=5, **kw), db.FP8ARModel(seed=5, **kw)
+    for m in (m1, m2):
+        for c in m.caches:
+            for buf in c.values():
+                buf.view(torch.uint8).zero_()
+    L = m1.tokens_per_chunk
+    g = torch.Generator(device=dev).manual_seed(21)
+    noise = [torch.randn(1, L, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(2)]
+    txt = torch.randn(1, Lt, 256, device=dev, generator=g).to(torch.bfloat16)
+    vecs = [torch.randn(1, 256, device=dev, generator=g).to(torch.bfloat16) for _ in range(4)]
+    tm = torch.ones(1, Lt, dtype=torch.bool, device=dev)
+    tm[0, 9:] = False
+    sig = torch.linspace(1.0, 0.0, 4).tolist()
+    x0 = m1.generate_chunk(noise[0], vecs[:3], vecs[3], sig, txt=txt, text_mask=tm)
+    assert m1.cache_valid_len == L + Lt
+    x1 = m1.generate_chunk(noise[1], vecs[:3], vecs[3], sig, txt=txt, text_mask=tm)
+    assert m1.cache_valid_len == 2 * (L + Lt) and m1.frames_done == 2
+    seg = torch.cat([torch.ones(L, dtype=torch.bool), tm[0].cpu()])
+    for c, mask in zip(m1.caches, m1.cache_masks):
+        assert torch.equal(mask[0, :2 * (L + Lt)].cpu(), torch.cat([seg, seg]))
+        assert not mask[0, 2 * (L + Lt):].any()
+        assert c["k"][:, :2 * (L + Lt)].view(torch.uint8).any()
+        assert not c["k"][:, 2 * (L + Lt):].view(torch.uint8).any()
+    y0 = m2.generate_chunk(noise[0], vecs[:3], vecs[3], sig, txt=txt, text_mask=tm)
+    assert torch.equal(x0, y0)                                  # deterministic
+    y1 = m2.generate_chunk(noise[1], vecs[:3], vecs[3], sig, txt=txt, text_mask=tm)
+    assert torch.equal(x1, y1)
+    m3 = db.FP8ARModel(seed=5, **kw)
+    m3.frames_done = 1                                         # same RoPE offset, empty cache
+    z1 = m3.generate_chunk(noise[1], vecs[:3], vecs[3], sig, txt=txt, text_mask=tm)
+    assert not torch.equal(x1, z1) and torch.isfinite(x1).all()  # history changes the result
+    with pytest.raises(ValueError, match="text tokens"):
+        m1.generate_chunk(noise[0], vecs[:3], vecs[3], sig)
+
+
+# ---------------------------------------------------------------------------
 # BASELINE config 4 at its own size, and the AR loop (config 5)
 
 def _ref_pre_rows(blk, img, vec, cos, sin, rows):
