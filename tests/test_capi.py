@@ -187,11 +187,15 @@ def test_ops_check_geometry_before_any_launch():
 
 
 def test_ar_model_refuses_a_chunk_past_capacity():
-    """FP8ARModel.generate_chunk checks cache_valid_len + chunk <= capacity
-    before running any pass."""
+    """FP8ARModel.generate_chunk checks cache_valid_len + the tokens a chunk
+    writes (image, plus text with the text stream) <= capacity before running
+    any pass."""
     dit = pkg_module("dit_block")
     m = dit.FP8ARModel.__new__(dit.FP8ARModel)
-    m.cache_valid_len, m.tokens_per_chunk, m.capacity = 20, 10, 25
+    m.cache_valid_len, m.tokens_per_chunk, m.write_tokens, m.capacity = 20, 10, 10, 25
+    with pytest.raises(ValueError, match="capacity"):
+        m.generate_chunk(None, [None], None, [1.0, 0.0])
+    m.cache_valid_len, m.write_tokens = 10, 16          # 10 image + 6 text tokens
     with pytest.raises(ValueError, match="capacity"):
         m.generate_chunk(None, [None], None, [1.0, 0.0])
 
