@@ -273,10 +273,11 @@ HN_DEVICE LaneOffs<NW> lane_offsets(const Params& p) {
 
 // `co` / `so`: a tile's byte offset inside descriptors that start before it
 // (the steady loop's span descriptors), added to every lane's code / scale
-// offset; 0 with per-tile descriptors.
+// offset; `mk0` the tile's first key in the span's validity bytes; 0 with
+// per-tile descriptors.
 template <int NW, bool MASK>
 HN_DEVICE void load_k(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& tb, int count, uint32_t co = 0,
-                      uint32_t so = 0) {
+                      uint32_t so = 0, int64_t mk0 = 0) {
     const uint32_t t = threadIdx.x;
     // Wave 0 reads the K scales, wave 1 the V scales. The wave index goes
     // through readfirstlane so that the descriptor choice is a scalar one (a
@@ -294,7 +295,7 @@ HN_DEVICE void load_k(const LaneOffs<NW>& lo, CacheRegs<NW>& r, const TileBase& 
     if constexpr (MASK) {
         if ((t >> 6) == 2u) {
             const uint32_t j = t & 63u;
-            r.mk = (int)j < count ? (tb.mk ? (uint32_t)tb.mk[j] : 1u) : 0u;
+            r.mk = (int)j < count ? (tb.mk ? (uint32_t)tb.mk[mk0 + j] : 1u) : 0u;
         }
     }
 }
@@ -819,7 +820,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
     // validity masks take the general loop throughout.
     const int64_t full_end = cache_end < wg_key_limit ? cache_end : wg_key_limit;
     const int n_full = full_end > 0 ? (int)(full_end / BKV) : 0;
-    const bool span_ok = !MASK && cache_end > 0 && p.cs1 > 0 && p.ss1 > 0 &&
+    const bool span_ok = cache_end > 0 && p.cs1 > 0 && p.ss1 > 0 &&
                          (cache_end - 1) * p.cs1 + D < ((int64_t)1 << 31) &&
                          ((cache_end - 1) * p.ss1 + 1) * 4 < ((int64_t)1 << 31);
     int t_fast = t_begin;
@@ -888,8 +889,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
             }
             int t = t_begin;
-            if constexpr (!MASK) {
-                // steady tiles (see t_fast): fetch tile t + 2 at offsets fco / fso
+            {
+                // steady tiles (see t_fast): fetch tile t + 2 at offsets fco / fso.
+                // With validity masks (MASK) each tile's word travels with its
+                // K write; a tile whose word is not all ones masks its blocks.
                 uint32_t fco = (uint32_t)((int64_t)(t + 2) * BKV * p.cs1);
                 uint32_t fso = (uint32_t)((int64_t)(t + 2) * BKV * p.ss1 * 4);
                 for (; t < t_fast; ++t) {
@@ -901,11 +904,19 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                     rebase(mxa, c, run, o);
                     sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
                     mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, nst, nsb);
-                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso);
+                    if constexpr (MASK) {
+                        store_mask<NW, MASK>(regs, nst);
+                        if (mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, BKV, mw);
+                    }
+                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso, (int64_t)(t + 2) * BKV);
                     __syncthreads();
                     rebase(mxb, c, run, o);
                     sa = step_a(sb, c, run.nm, run.l, pf, nst + ka_off, qf);
                     mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, nst, nsb);
+                    if constexpr (MASK) {
+                        mw = tile_mask<MASK>(nst);  // tile t + 1
+                        if (mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, BKV, mw);
+                    }
                     if (threadIdx.x < 2 * BKV) sbuf[(u & 1) * SB_FLOATS + threadIdx.x] = regs.s;
                     load_v<NW>(lo, regs, span, fco);
                     __syncthreads();
@@ -1001,8 +1012,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
             mxa = raw_max(sa);
                 if (!g.full || mw != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(g), mw);
             int t = t_begin;
-            if constexpr (!MASK) {
+            {
                 // steady tiles (see t_fast): fetch tile t + NS at offsets fco / fso
+                // (validity words as in the two-stage loop above)
                 uint32_t fco = (uint32_t)((int64_t)(t + NS) * BKV * p.cs1);
                 uint32_t fso = (uint32_t)((int64_t)(t + NS) * BKV * p.ss1 * 4);
                 int s0 = 0;  // stage of tile t, (t - t_begin) % NS
@@ -1015,13 +1027,22 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                     uint8_t* wst = smem + sw * STAGE;
                     const float* wsb = sbuf + ((u + NS - 1) & 1) * SB_FLOATS;
                     f16x8 pf[2];
+                    const uint64_t mwn = tile_mask<MASK>(st1);  // tile t + 1
                     rebase(mxa, c, run, o);
                     sb = step_a(sa, c, run.nm, run.l, pf, st + ka_off + 32 * KROW, qf);
                     mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
-                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso);
+                    if constexpr (MASK) {
+                        store_mask<NW, MASK>(regs, wst);
+                        if (mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, BKV, mw);
+                    }
+                    load_k<NW, MASK>(lo, regs, span, BKV, fco, fso, (int64_t)(t + NS) * BKV);
                     rebase(mxb, c, run, o);
                     sa = step_a(sb, c, run.nm, run.l, pf, st1 + ka_off, qf);
                     mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
+                    if constexpr (MASK) {
+                        if (mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, BKV, mwn);
+                        mw = mwn;
+                    }
                     if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
                     load_v<NW>(lo, regs, span, fco);
                     __syncthreads();

@@ -79,6 +79,9 @@ def _linear_fake(x, weight, scale):
     return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.bfloat16)
 
 
+SCALE_ROW_SPAN = 2.0 ** 60
+
+
 def validate_serialized_tensors(weight: torch.Tensor, scale: torch.Tensor, expected_shape) -> None:
     """A serialized FP8 layer is valid when its [out, in] shape is the expected
     one with both dims multiples of 128, the codes are e4m3, and the scales are
@@ -92,6 +95,12 @@ def validate_serialized_tensors(weight: torch.Tensor, scale: torch.Tensor, expec
         raise ValueError("Invalid serialized FP8 weight/scale")
     if not bool(torch.isfinite(scale).all()) or not bool((scale > 0).all()):
         raise ValueError("FP8 scales must be finite and positive")
+    # The blockwise GEMM carries its accumulators in units of the current K
+    # block's factor; a weight scale row spanning more than 2^60 could, with
+    # the activation scales, push the rescale past fp32's range.
+    row_span = scale.amax(dim=1) / scale.amin(dim=1)
+    if bool((row_span > SCALE_ROW_SPAN).any()):
+        raise ValueError("FP8 scales of one output block row span more than 2^60")
 
 
 def _inference_input(module: nn.Module, x: torch.Tensor) -> torch.Tensor:

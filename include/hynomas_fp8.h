@@ -143,6 +143,14 @@ int hn_gemm_fp8_rowcol(const void *a, const void *b, const float *sa, const floa
  *   out[m, n] = bf16( sum_kb sa[m/128, kb] * sb[n/128, kb] * sum_{k in kb} a[m,k] b[n,k] )
  * a: e4m3 [M, K]; b: e4m3 [N, K]; sa: fp32 [ceil(M/128), K/128]; sb: fp32
  * [N/128, K/128]; out: bf16 [M, N] contiguous. N % 128 == 0, K % 128 == 0.
+ * Range: the accumulators are carried in units of the current K block's
+ * factor f = sa * sb (rescaled by f_prev / f between blocks), so the result
+ * stays finite while, within each 128 x 128 output block, no earlier factor
+ * exceeds a later one by 2^99 or more (then |acc| < 24 K blocks x 2.6e7 x
+ * 2^99 would stay below FLT_MAX; past it the rescale overflows to Inf). The
+ * FP8Linear loader refuses weight scale rows spanning more than 2^60
+ * (pixelumm_fp8.validate_serialized_tensors); activation scales from the
+ * blockwise quantizer span more only for bf16 blocks 2^60 apart in magnitude.
  * Replaces gemm / pixel_gemm, hymm/models/vae/pixelumm_decoder/csrc/cutlass_fp8.cu:20-57
  * and reactor/hy_nomas_fp8_sm100.cu:67-107. */
 int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const float *sb,
@@ -176,6 +184,11 @@ int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const f
  * the reference's dequantized values bf16(code * scale); query rows that see
  * no key are written as zeros (range_attention.py:212-239). The probabilities
  * multiply V as fp16 (relative rounding 2^-11) with fp32 accumulation.
+ * Range: V (cached values bf16(code * scale) and the bf16 tail) is held as
+ * fp16, converted toward zero, so a V value of magnitude above 65504 enters
+ * the product as +-65504 (the reference attends the bf16 value); every other
+ * bf16 V value is exact in fp16 down to 2^-24. A cached V exceeds 65504 only
+ * when the written row held such a value (|bf16(code * s)| <= amax).
  * workspace: device scratch of at least hn_attn_fp8kv_workspace_size(...)
  *        bytes (16-byte aligned; NULL/0 when that size is 0). It holds per-split
  *        partial results when the key range is split across workgroups to fill

@@ -261,6 +261,12 @@ def test_serialized_fp8_validation_and_dtype_preserving_apply():
         pf.FP8Linear.from_quantized(w, s, (256, 100))
     with pytest.raises(ValueError, match="positive"):
         pf.FP8Linear.from_quantized(w, torch.zeros(2, 1), (256, 128))
+    # a scale row spanning more than 2^60 is refused: the blockwise GEMM's
+    # carried rescale f_prev / f must stay inside fp32
+    w2 = torch.zeros(128, 384, dtype=torch.float8_e4m3fn)
+    pf.validate_serialized_tensors(w2, torch.tensor([[1.0, 2.0 ** 60, 1.0]]), (128, 384))  # span 2^60
+    with pytest.raises(ValueError, match="2\\^60"):
+        pf.validate_serialized_tensors(w2, torch.tensor([[0.5, 2.0 ** 60, 1.0]]), (128, 384))  # 2^61
     m.train()
     with pytest.raises(RuntimeError, match="inference"):
         m(torch.zeros(4, 128, dtype=torch.bfloat16))

@@ -669,3 +669,37 @@ def test_pipeline_fp8_storage_write_and_audit(O, dev):
     finally:
         attn_hook.uninstall()
         store_hook.uninstall()
+
+
+def test_v_beyond_fp16_range_enters_as_65504(O, dev):
+    """The documented range of the PV product: V is held as fp16, converted
+    toward zero, so cached or tail V values past 65504 in magnitude enter as
+    +-65504 (include/hynomas_fp8.h, hn_attn_fp8kv); everything else is the
+    reference's bf16 value. Checked against the oracle with V clipped there,
+    and shown to differ from attention over the unclipped values."""
+    kvc = pkg_module("fp8_kv_cache")
+    ca = pkg_module("cache_attention")
+    H, D, n, Lc, Lq = 2, 128, 64, 40, 32
+    g = torch.Generator(device=dev).manual_seed(77)
+    k = torch.randn(1, n, H, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, n, H, D, device=dev, generator=g)
+    v[0, 5, 0, :8] = 1.0e5                       # a cached row holding values past fp16's range
+    v[0, 9, 1, 3] = -9.0e4
+    cache = kvc.make_fp8_kv_block(1, n, H, D, device=dev)
+    kvc.quantize_kv_pair_into(cache, k, v.to(torch.bfloat16), 0)
+    kc = torch.randn(1, Lc, H, D, device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn(1, Lc, H, D, device=dev, generator=g)
+    vc[0, 3, :, 10:20] = 7.0e4                   # and tail values
+    vc = vc.to(torch.bfloat16)
+    q = (torch.randn(1, Lq, H, D, device=dev, generator=g) * 3).to(torch.bfloat16)
+    out = ca.chunk_attention(q, cache, n, k_cur=kc, v_cur=vc)
+    kh, vh = _dequant(O, cache, n)
+    kall = np.concatenate([kh, O.bf16_bits_to_f32(bf16_bits(kc[0]))], 0)
+    vall = np.concatenate([vh, O.bf16_bits_to_f32(bf16_bits(vc[0]))], 0)
+    assert np.abs(vall).max() > 65504.0
+    qf = O.bf16_bits_to_f32(bf16_bits(q[0]))
+    got = out[0].float().cpu().numpy()
+    ref = O.attention_reference(qf, kall, np.clip(vall, -65504.0, 65504.0))
+    assert_close_bf16(got, ref, what="V clipped at 65504")
+    unclipped = O.attention_reference(qf, kall, vall)
+    assert np.abs(unclipped - got).max() > 1.0

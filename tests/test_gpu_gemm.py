@@ -211,6 +211,27 @@ def test_blockwise_gemm_zero_block_factors(O, dev):
     _blockwise_check(got, expected)
 
 
+@pytest.mark.parametrize("direction", ["up", "down"])
+def test_blockwise_gemm_factor_jump_of_2_to_60(O, dev, direction):
+    """Adjacent K blocks whose weight factors differ by 2^60, the widest span
+    the FP8Linear loader accepts: the carried accumulator's rescale by
+    f_prev / f (2^60 or 2^-60 here) stays finite, and the result matches the
+    float64 dequantize-then-matmul reference."""
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator().manual_seed(31)
+    a = torch.randn(256, 512, generator=g).to(torch.bfloat16)
+    b = torch.randn(256, 512, generator=g).to(torch.bfloat16)
+    qa, sa = pf._quantize_blockwise(a.to(dev))
+    qb, sb = pf._quantize_blockwise(b.to(dev))
+    jump = 2.0 ** 60 if direction == "up" else 2.0 ** -60
+    sb[:, 2:] *= jump                                  # K blocks 2, 3 against 0, 1
+    pf.validate_serialized_tensors(qb, sb, (256, 512))  # within the loader's bound
+    got = pf.load_extension().gemm(qa, qb, sa, sb)
+    assert torch.isfinite(got.float()).all()
+    expected = O.blockwise_gemm_reference(u8(qa), sa.cpu().numpy(), u8(qb), sb.cpu().numpy())
+    _blockwise_check(got, expected)
+
+
 def test_blockwise_gemm_contract_errors(dev):
     pf = pkg_module("pixelumm_fp8")
     ext = pf.load_extension()
