@@ -1207,12 +1207,16 @@ static int attn_splits(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int64_t
 // workgroups, 1 per CU, 256 queries each -- the 8-wave round measures 0.92 of
 // it at 86400 keys, so K8_ROUND = 0.92):
 //   4-wave only: ceil(n4 / 2C) rounds, n4 = B H ceil(Lq / 128);
-//   8-wave:      ceil(n8 / C) K8_ROUND rounds, n8 = B H floor(Lq / 256), plus
-//                the leftover rows on the 4-wave kernel, split sp ways:
-//                ceil(nr sp / 2C) / sp rounds.
-// The 8-wave kernel is used only when it fills every CU at least once
-// (n8 >= C) and the model says it is faster: a partial last round of 1-per-CU
-// workgroups idles half the SIMD slots a 4-wave round would keep busy.
+//   8-wave over k tiles of 256 rows per (batch, head): ceil(B H k / C)
+//                K8_ROUND rounds, plus the other Lq - 256 k rows on the
+//                4-wave kernel, split sp ways: ceil(nr sp / 2C) / sp rounds.
+// Every k from floor(Lq / 256) down is tried, so that a few rows past a
+// whole number of 8-wave rounds (a chunk's text tokens beside its 10 800
+// image tokens: 43 tiles x 24 heads = 4.03 rounds, i.e. 5) go to the split
+// 4-wave launch instead of a nearly empty extra round. The 8-wave kernel is
+// used only when it fills every CU at least once (B H k >= C) and the model
+// says it is faster: a partial last round of 1-per-CU workgroups idles half
+// the SIMD slots a 4-wave round would keep busy.
 struct AttnPlan {
     int64_t rows8;
     int splits;
@@ -1223,19 +1227,23 @@ static AttnPlan attn_plan(int64_t B, int64_t Lq, int64_t H, int64_t kv_len, int6
     const int cus = device_cus();
     AttnPlan plan{0, 1};
     const int64_t bh = B * H;
-    const int64_t n8 = bh * (Lq / attn::Shape<8>::BQ);
-    if (n8 >= cus) {
-        const int64_t n4 = bh * ((Lq + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ);
-        const double r4 = (double)((n4 + 2 * cus - 1) / (2 * cus));
+    const int64_t n4 = bh * ((Lq + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ);
+    double best = (double)((n4 + 2 * cus - 1) / (2 * cus));
+    for (int64_t k = Lq / attn::Shape<8>::BQ; k > 0 && bh * k >= cus; --k) {
+        const int64_t n8 = bh * k;
         double r8 = K8_ROUND * (double)((n8 + cus - 1) / cus);
-        const int64_t rows8 = (Lq / attn::Shape<8>::BQ) * attn::Shape<8>::BQ;
+        const int64_t rows8 = k * attn::Shape<8>::BQ;
         const int64_t rest = Lq - rows8;
         if (rest > 0) {
             const int sp = attn_splits(B, rest, H, kv_len, cur_len, cus);
             const int64_t nr = bh * ((rest + attn::Shape<4>::BQ - 1) / attn::Shape<4>::BQ) * sp;
             r8 += (double)((nr + 2 * cus - 1) / (2 * cus)) / sp;
         }
-        if (r8 < r4) plan.rows8 = rows8;
+        if (r8 < best) {
+            best = r8;
+            plan.rows8 = rows8;
+        }
+        if (r8 > best + 1.0) break;  // fewer tiles only add 4-wave rounds from here
     }
     plan.splits = attn_splits(B, Lq - plan.rows8, H, kv_len, cur_len, cus);
     return plan;
