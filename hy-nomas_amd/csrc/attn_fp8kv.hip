@@ -428,18 +428,24 @@ HN_DEVICE void store_tile(const CacheRegs<NW>& r, uint8_t* st, const float* sb) 
 
 // Unquantized tail tile (bf16 K/V of the current chunk), written with the
 // same thread-to-location mapping as the cache writes (so it cleanly
-// replaces what those wrote to the same stage). Not prefetched: it is at most
-// one chunk of the keys.
+// replaces what those wrote to the same stage). The loads and the LDS writes
+// are separate steps: the 8-wave loop issues a tail tile's loads one tile
+// ahead, as it does a cache tile's, into TailRegs; the 4-wave loop (two
+// stages, registers already near the limit) loads and writes in one go.
+template <int NW>
+struct TailRegs {
+    uint4 k[2 * Shape<NW>::KU];        // unit i: dims 16 u .. + 7 in k[2 i], + 8 .. + 15 in k[2 i + 1]
+    uint32_t v[4][Shape<NW>::VD / 2];  // dims VD dg .. + VD - 1 of quad key j (bf16 pairs)
+    uint32_t mk;                       // MASK: validity of key t - 128 (wave 2)
+};
+
 template <int NW, bool MASK>
-HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
+HN_DEVICE void load_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, TailRegs<NW>& r) {
     const int t = threadIdx.x;
     if constexpr (MASK) {
         if ((t >> 6) == 2) {
             const int j = t & 63;
-            uint32_t ok = 0u;
-            if (j < count) ok = p.uvalid ? (uint32_t)p.uvalid[b * p.uvs + first + j] : 1u;
-            const uint64_t bits = __ballot(ok != 0u);
-            if (j == 0) *reinterpret_cast<uint64_t*>(st + MASK_OFF) = bits;
+            r.mk = j < count ? (p.uvalid ? (uint32_t)p.uvalid[b * p.uvs + first + j] : 1u) : 0u;
         }
     }
 #pragma unroll
@@ -447,42 +453,76 @@ HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first,
         const int key = (int)k_key(t) + (Shape<NW>::NT / 8) * i, unit = (int)k_unit(t);
         const int j = min(key, count - 1);
         const uint16_t* src = p.kcur + b * p.us0 + (first + j) * p.us1 + h * p.us2 + unit * 16;
-        const uint4 lo = *reinterpret_cast<const uint4*>(src);
-        const uint4 hi = *reinterpret_cast<const uint4*>(src + 8);
+        r.k[2 * i] = *reinterpret_cast<const uint4*>(src);
+        r.k[2 * i + 1] = *reinterpret_cast<const uint4*>(src + 8);
+    }
+}
+
+template <int NW, bool MASK>
+HN_DEVICE void store_tail_k(const TailRegs<NW>& r, uint8_t* st) {
+    const int t = threadIdx.x;
+    if constexpr (MASK) {
+        if ((t >> 6) == 2) {
+            const uint64_t bits = __ballot(r.mk != 0u);
+            if ((t & 63) == 0) *reinterpret_cast<uint64_t*>(st + MASK_OFF) = bits;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < Shape<NW>::KU; ++i) {
+        const int key = (int)k_key(t) + (Shape<NW>::NT / 8) * i, unit = (int)k_unit(t);
         uint4* dst = reinterpret_cast<uint4*>(st + key * KROW + unit * 32);
-        dst[0] = lo;
-        dst[1] = hi;
+        dst[0] = r.k[2 * i];
+        dst[1] = r.k[2 * i + 1];
     }
 }
 
 template <int NW>
-HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
+HN_DEVICE void load_tail_v(const Params& p, int64_t b, int64_t h, int64_t first, int count, TailRegs<NW>& r) {
     constexpr int VD = Shape<NW>::VD;
     const int qd = threadIdx.x & 15, dg = v_group<NW>();
-    uint32_t w[4][VD / 2];  // dims VD dg .. + VD - 1 of quad key j (bf16 pairs)
-    // V^T holds fp16: the bf16 values converted (exactly, in fp16's range).
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int key = min(quad_key(qd, j), count - 1);
         const uint16_t* src = p.vcur + b * p.us0 + (first + key) * p.us1 + h * p.us2 + VD * dg;
         if constexpr (VD == 8) {
             const uint4 x = *reinterpret_cast<const uint4*>(src);
-            w[j][0] = x.x; w[j][1] = x.y; w[j][2] = x.z; w[j][3] = x.w;
+            r.v[j][0] = x.x; r.v[j][1] = x.y; r.v[j][2] = x.z; r.v[j][3] = x.w;
         } else {
             const uint2 x = *reinterpret_cast<const uint2*>(src);
-            w[j][0] = x.x; w[j][1] = x.y;
+            r.v[j][0] = x.x; r.v[j][1] = x.y;
         }
     }
+}
+
+// V^T holds fp16: the bf16 values converted (exactly, in fp16's range).
+template <int NW>
+HN_DEVICE void store_tail_v(const TailRegs<NW>& r, uint8_t* st) {
+    constexpr int VD = Shape<NW>::VD;
+    const int qd = threadIdx.x & 15, dg = v_group<NW>();
 #pragma unroll
     for (int d = 0; d < VD; ++d) {
         uint32_t o[2];
         const uint32_t sh = (d & 1) * 16;
 #pragma unroll
         for (int pr = 0; pr < 2; ++pr)
-            o[pr] = bf16x2_to_f16x2(((w[2 * pr][d >> 1] >> sh) & 0xffffu) |
-                                    (((w[2 * pr + 1][d >> 1] >> sh) & 0xffffu) << 16));
+            o[pr] = bf16x2_to_f16x2(((r.v[2 * pr][d >> 1] >> sh) & 0xffffu) |
+                                    (((r.v[2 * pr + 1][d >> 1] >> sh) & 0xffffu) << 16));
         *reinterpret_cast<uint2*>(st + K_BYTES + (VD * dg + d) * VTROW + 8 * qd) = make_uint2(o[0], o[1]);
     }
+}
+
+template <int NW, bool MASK>
+HN_DEVICE void copy_tail_k(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
+    TailRegs<NW> r;
+    load_tail_k<NW, MASK>(p, b, h, first, count, r);
+    store_tail_k<NW, MASK>(r, st);
+}
+
+template <int NW>
+HN_DEVICE void copy_tail_v(const Params& p, int64_t b, int64_t h, int64_t first, int count, uint8_t* st) {
+    TailRegs<NW> r;
+    load_tail_v<NW>(p, b, h, first, count, r);
+    store_tail_v<NW>(r, st);
 }
 
 HN_DEVICE f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
@@ -993,12 +1033,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                     copy_tail_v<NW>(p, b, h, gk.first, gk.count, smem + k * STAGE);
                 }
             }
+            TailRegs<NW> tregs;  // a tail tile's bf16 K/V, loaded one tile ahead of its write
             if (t_begin + NS - 1 < t_end) {
                 const Geom gk = geom(t_begin + NS - 1);
                 if (gk.cache) {
                     const TileBase tb = tile_base(p, b, h, gk.first, gk.count);
                     load_k<NW, MASK>(lo, regs, tb, gk.count);
                     load_v<NW>(lo, regs, tb);
+                } else {
+                    load_tail_k<NW, MASK>(p, b, h, gk.first, gk.count, tregs);
+                    load_tail_v<NW>(p, b, h, gk.first, gk.count, tregs);
                 }
             }
             // Everything issued so far (the Q fragments included) has landed;
@@ -1076,9 +1120,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 mxb = step_b<FMT, NW, 1>(pf, st + va_off, 0, o, sb, regs, wst, wsb);
                 store_mask<NW, MASK>(regs, wst);
                 if (!g.full || mw != ALL_KEYS) mxb = mask_raw(sb, 1, half, lim_of(g), mw);
-                if (write && !gw.cache) copy_tail_k<NW, MASK>(p, b, h, gw.first, gw.count, wst);
+                if (write && !gw.cache) store_tail_k<NW, MASK>(tregs, wst);
                 const int nf = fetch && gf.cache ? gf.count : 0;  // 0: no fetch (zeros)
                 load_k<NW, MASK>(lo, regs, tile_base(p, b, h, gf.first, nf), nf);
+                if (fetch && !gf.cache) load_tail_k<NW, MASK>(p, b, h, gf.first, gf.count, tregs);
 
                 // ---- half 1 (on the last tile the S block of "tile t + 1" reads
                 // stale LDS; its result is never used)
@@ -1086,10 +1131,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_fp8kv_kernel(Params p) {
                 sa = step_a(sb, c, run.nm, run.l, pf, st1 + ka_off, qf);
                 mxa = step_b<FMT, NW, 2>(pf, st + va_off, 1, o, sa, regs, wst, wsb);
                 if (!gn.full || mwn != ALL_KEYS) mxa = mask_raw(sa, 0, half, lim_of(gn), mwn);
-                if (write && !gw.cache) copy_tail_v<NW>(p, b, h, gw.first, gw.count, wst);
+                if (write && !gw.cache) store_tail_v<NW>(tregs, wst);
                 // (without a fetch: zeros into a scale buffer no write reads)
                 if (threadIdx.x < 2 * BKV) sbuf[((u + NS) & 1) * SB_FLOATS + threadIdx.x] = regs.s;
                 load_v<NW>(lo, regs, tile_base(p, b, h, gf.first, nf));
+                if (fetch && !gf.cache) load_tail_v<NW>(p, b, h, gf.first, gf.count, tregs);
                 __syncthreads();
                 g = gn;
                 mw = mwn;
