@@ -22,6 +22,7 @@ block must stay within that movement (times 1.5, plus the bf16 output's own
 rounding)."""
 import math
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -603,12 +604,19 @@ def test_ar_loop_against_cpu_restatement(O, dev):
     """Two chunks of a 2-block, hidden-256 model against the CPU restatement of
     the loop: per chunk 3 Euler denoising passes and one write pass at the
     chunk's RoPE offset, then the valid length advances. The latents agree
-    within 2e-2 rel-L2, and each layer's written cache rows, decoded, hold
-    the restatement's write-pass K/V up to e4m3 rounding: per element at most
-    2^-4 relative of the row's scale grid, about 2.5e-2 rel-L2 in all (the
-    codes themselves are bit-exact for given inputs, pinned by the KV-write
-    tests; here the inputs differ by the chunk's bf16 roundings, which moves
-    codes near their rounding boundaries)."""
+    within the north star's 1e-2 rel-L2.
+
+    The cache rows each layer wrote are then explained stage by stage. Replayed
+    on the GPU from the write pass's own input (the final latent, layer by
+    layer; the write pass attends the same keys as a pass without a write),
+    each layer's K/V quantize, through the oracle, to exactly the codes and
+    scales in the cache: the write itself is exact. What separates the cache
+    from the restatement is only that its K/V inputs have drifted: the GPU's
+    write-pass K/V against the restatement's, bf16 against bf16, differ by the
+    same rel-L2 as the decoded cache does (about 3e-2 at this width: four
+    quantizers deep, a one-ulp bf16 difference at a quantizer's input moves
+    an e4m3 code by up to 2^-3, and small elements span many e4m3 steps of
+    their row's scale grid)."""
     print("case ar loop parity", flush=True)
     db = pkg_module("dit_block")
     kw = dict(depth=2, hidden=256, heads=2, latent_shape=(1, 4, 5), max_chunks=3, device=dev)
@@ -627,14 +635,29 @@ def test_ar_loop_against_cpu_restatement(O, dev):
         assert m.cache_valid_len == valid + L and m.frames_done == frames + 1
         rel = _rel(x.float(), rx.float())
         print(f"chunk {chunk}: latent rel-L2 {rel:.3e}", flush=True)
-        assert torch.isfinite(x.float()).all() and rel <= 2e-2
-        for layer, (cache, (rk, rv)) in enumerate(zip(m.caches, rw)):
-            for name, want in (("k", rk), ("v", rv)):
+        assert torch.isfinite(x.float()).all() and rel <= 1e-2
+        h = x
+        for layer, (blk, cache, (rk, rv)) in enumerate(zip(m.blocks, m.caches, rw)):
+            with torch.no_grad():
+                _, gk, gv, _ = blk.pre_attention(h, vecs[3], cos, sin)
+                gk, gv = gk.clone(), gv.clone()
+                h = blk(h, vecs[3], cos, sin, cache, valid, update_cache=False)
+            for name, own, want in (("k", gk, rk), ("v", gv, rv)):
+                qo, so = O.kv_quantize(bf16_bits(own))
+                assert np.array_equal(u8(cache[name][:, valid:valid + L]), qo), (layer, name, "codes")
+                got_s = cache[name + "_scale"][:, valid:valid + L].cpu().numpy()
+                assert np.array_equal(got_s.view(np.uint32), so.view(np.uint32)), (layer, name, "scales")
                 dec = (cache[name][:, valid:valid + L].float()
                        * cache[name + "_scale"][:, valid:valid + L]).cpu()
-                r = _rel(dec, want.float())
-                print(f"  layer {layer} {name}: decoded cache vs restated K/V rel-L2 {r:.3e}", flush=True)
-                assert r <= 4e-2, (layer, name, r)
+                qr, sr = O.kv_quantize(bf16_bits(want.to(torch.bfloat16)))
+                dec_ref = torch.from_numpy(O.e4m3_decode(qr) * sr)     # the restatement's own cache rows
+                r_in = _rel(own.float(), want.float())                  # drift of the K/V inputs
+                r_cache = _rel(dec, dec_ref)                            # the same, after quantization
+                r_q = _rel(dec_ref, want.float())                       # e4m3's own rounding
+                print(f"  layer {layer} {name}: codes = oracle(GPU write-pass K/V) exactly; K/V inputs "
+                      f"GPU vs restated rel-L2 {r_in:.3e}, their caches {r_cache:.3e} "
+                      f"(e4m3 rounding alone {r_q:.3e})", flush=True)
+                assert r_in <= 2e-2 and r_cache <= 2 * r_in + 1e-2, (layer, name, r_in, r_cache)
 
 
 def test_config5_ar_chunk_at_full_size(dev):
