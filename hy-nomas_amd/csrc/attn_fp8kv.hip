@@ -641,11 +641,9 @@ HN_DEVICE void pin(A& a) {
 // The two software-pipelined steps of a half tile. Each pairs one 8-MFMA chain
 // with the independent VALU work of the other chain, spread over 8 slots (one
 // MFMA + about 8 VALU instructions, ~32 cycles each) that sched_barrier keeps
-// in place: on gfx950 a wave's VALU instructions execute while its own MFMAs
-// occupy the matrix core (about 4 per 32-cycle MFMA for free), while another
-// wave's VALU work slows the MFMAs nearly as much as running it serially
-// (hy-nomas_amd/probes/issue_rates.hip measures both), so the overlap has to
-// be built into each wave's instruction stream. Operand reads from LDS are
+// in place: a wave's VALU instructions execute while its own MFMAs occupy the
+// matrix core, so the overlap is built into each wave's instruction stream
+// rather than left to the other wave on the SIMD. Operand reads from LDS are
 // issued two slots ahead.
 
 // Step A: S^T of the next block from the K rows at ka (this lane's row in the

@@ -69,8 +69,10 @@ HN_DEVICE uint32_t e4m3_encode(float f) {
 // conversion v_cvt_pk_fp8_f32 (OCP e4m3, round to nearest even). On every
 // finite |x| <= 448.5 -- the only inputs the quantizers produce, since
 // |x / s| <= 448 (1 + 2^-23) for s = amax / 448 -- it returns exactly
-// e4m3_encode(x); that equivalence was checked exhaustively over all fp32
-// bit patterns of that range, both signs, on the device.
+// e4m3_encode(x); that equivalence is checked exhaustively over all fp32
+// bit patterns of that range, both signs, on the device
+// (tests/test_gpu_quant.py::test_hardware_e4m3_conversion_matches_oracle_over_quantizer_range,
+// through hn_e4m3_encode_range).
 HN_DEVICE uint32_t e4m3_encode4(float a, float b, float c, float d) {
     int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
     w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
