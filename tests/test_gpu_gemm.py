@@ -223,9 +223,18 @@ def test_blockwise_gemm_factor_jump_of_2_to_60(O, dev, direction):
     b = torch.randn(256, 512, generator=g).to(torch.bfloat16)
     qa, sa = pf._quantize_blockwise(a.to(dev))
     qb, sb = pf._quantize_blockwise(b.to(dev))
-    jump = 2.0 ** 60 if direction == "up" else 2.0 ** -60
-    sb[:, 2:] *= jump                                  # K blocks 2, 3 against 0, 1
+    # K blocks 2, 3 at exactly 2^60 (2^-60) times the row's smallest (largest)
+    # factor of blocks 0, 1: the row span is then 2^60, the loader's bound
+    if direction == "up":
+        sb[:, 2:] = sb[:, :2].amin(dim=1, keepdim=True) * 2.0 ** 60
+    else:
+        sb[:, 2:] = sb[:, :2].amax(dim=1, keepdim=True) * 2.0 ** -60
+    span = sb.amax(dim=1) / sb.amin(dim=1)
+    assert bool((span == 2.0 ** 60).all()), span
     pf.validate_serialized_tensors(qb, sb, (256, 512))  # within the loader's bound
+    with pytest.raises(ValueError, match="span more than 2"):
+        pf.validate_serialized_tensors(qb, sb * torch.tensor([1.0, 1.0, 2.0, 2.0], device=dev) ** (
+            1 if direction == "up" else -1), (256, 512))
     got = pf.load_extension().gemm(qa, qb, sa, sb)
     assert torch.isfinite(got.float()).all()
     expected = O.blockwise_gemm_reference(u8(qa), sa.cpu().numpy(), u8(qb), sb.cpu().numpy())
