@@ -181,11 +181,13 @@ def ln_modulate_bf16(x_bits: np.ndarray, shift_bits: np.ndarray, scale_bits: np.
 
     inv_cols = np.float32(1.0) / np.float32(cols)
     xc = x.reshape(rows, nch, 8)
-    mean = (wave_sum(xc) * inv_cols).astype(np.float32)
-    d = (xc - mean[:, None, None]).astype(np.float32)
-    var = (wave_sum((d * d).astype(np.float32)) * inv_cols).astype(np.float32)
-    rstd = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
-    y = bf16_bits_to_f32(f32_to_bf16_bits((d * rstd[:, None, None]).astype(np.float32).reshape(rows, cols)))
+    # rows holding Inf or NaN give NaN (inf - inf), as the kernel's fp32 ops do
+    with np.errstate(invalid="ignore", over="ignore"):
+        mean = (wave_sum(xc) * inv_cols).astype(np.float32)
+        d = (xc - mean[:, None, None]).astype(np.float32)
+        var = (wave_sum((d * d).astype(np.float32)) * inv_cols).astype(np.float32)
+        rstd = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+        y = bf16_bits_to_f32(f32_to_bf16_bits((d * rstd[:, None, None]).astype(np.float32).reshape(rows, cols)))
     b = np.arange(rows) // rpb
     sc = bf16_bits_to_f32(np.asarray(scale_bits, dtype=np.uint16))[b]
     sh = bf16_bits_to_f32(np.asarray(shift_bits, dtype=np.uint16))[b]
