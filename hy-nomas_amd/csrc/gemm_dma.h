@@ -147,5 +147,25 @@ HN_GEMM_HD bool tile_of_slot(const Q& p, int x, int i, int S, int& tm, int& tn) 
     return tile_at(p, x, fx + q, tm, tn);
 }
 
+// A wave's share of a tile: the 32-column blocks (imax) and 32-row blocks
+// (jmax) that hold any output inside the M x N matrix -- what its MFMAs
+// compute and its bounds-checked stores cover -- and whether its whole
+// 128-row x wc-column sub-tile is inside the matrix (`inside`), which is what
+// lets its direct stores skip the bounds test. jmax = 4 does not imply
+// inside: a wave with 97..127 rows left still has four row blocks.
+struct WaveExtent {
+    int imax, jmax;
+    bool inside;
+};
+
+HN_GEMM_HD WaveExtent wave_extent(int64_t M, int64_t N, int64_t row0, int64_t col0, int wc) {
+    const int64_t rows = M - row0, cols = N - col0;
+    WaveExtent e;
+    e.jmax = rows >= 128 ? 4 : (rows <= 0 ? 0 : (int)((rows + 31) >> 5));
+    e.imax = cols >= wc ? wc / 32 : (cols <= 0 ? 0 : (int)(cols >> 5));
+    e.inside = rows >= 128 && cols >= wc;
+    return e;
+}
+
 }  // namespace gemm
 }  // namespace hn

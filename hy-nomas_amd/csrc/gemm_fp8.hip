@@ -881,7 +881,12 @@ HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, i
 // bytes, without the LDS staging of the carried passes: the 8 stores of a
 // pass write every byte of its 32 rows' 128-byte lines, which the L2 merges.
 // (Measured with bias + GELU: 387 against 393 us through the staging area.)
-template <int ACT, int WC>
+// CHECK: stores only inside the matrix. A wave whose whole sub-tile is
+// inside (WaveExtent::inside) passes false: without the per-store branch the
+// 32 four-value groups are one basic block whose independent chains the
+// compiler interleaves (with it, each group ran alone as a dependent chain of
+// about 60 instructions).
+template <int ACT, int WC, bool CHECK>
 HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, int64_t m0,
                              int64_t n0, int wm, int wn, int lane) {
     const int h = lane >> 5, r = lane & 31;
@@ -919,7 +924,7 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
                 }
                 const int64_t m = m0 + wm * 128 + 32 * j + r;
                 const int64_t n = n0 + wn * WC + nl;
-                if (m < p.M && n < p.N) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
+                if (!CHECK || (m < p.M && n < p.N)) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
             }
     }
 }
@@ -979,14 +984,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
     // 32 rows). Wave-uniform. Tiles with every block inside the matrix take
     // the carried path.
+    // cinside: the wave's whole sub-tile is inside (its direct stores go
+    // unchecked).
     int64_t cm0 = 0, cn0 = 0;
     int cimax = 0, cjmax = 0;
+    bool cinside = false;
     auto set_cur = [&](int tm_, int tn_) {
         cm0 = (int64_t)tm_ * BM;
         cn0 = (int64_t)tn_ * TBN;
-        const int64_t rows_w = p.M - (cm0 + wm * 128), cols_w = p.N - (cn0 + wn * WC);
-        cjmax = rows_w >= 128 ? 4 : (rows_w <= 0 ? 0 : (int)((rows_w + 31) >> 5));
-        cimax = cols_w >= WC ? WC / 32 : (cols_w <= 0 ? 0 : (int)(cols_w >> 5));
+        const WaveExtent e = wave_extent(p.M, p.N, cm0 + wm * 128, cn0 + wn * WC, WC);
+        cimax = e.imax;
+        cjmax = e.jmax;
+        cinside = e.inside;
     };
     int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
     auto pair_of = [&](int s) { return (s + par) & 1; };
@@ -1186,7 +1195,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
         }
-        direct_passes<ACT, WC>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
+        if (cinside) direct_passes<ACT, WC, false>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
+        else direct_passes<ACT, WC, true>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
         convert_tile(acc, y, prm, fresh_lane());
         pm0 = cm0;
         pn0 = cn0;

@@ -3,10 +3,16 @@
 // exactly as gemm_rowcol_oe_kernel does (workgroup `slot` of XCD x starts at
 // queue entry slot and steps by S, the workgroups per XCD, until the first
 // entry without a tile) and counts how often each output tile is produced.
+// For every wave of every tile it also takes wave_extent (the same header)
+// and, where the wave counts as inside, walks the stores its unchecked direct
+// passes make -- rows 32 j + r (j = 2, 3; r < 32), columns 32 i + 8 vq + 4 h
+// + e (i < wc / 32) of its sub-tile -- and counts those outside M x N; and it
+// checks that the blocks below (imax, jmax) cover every output of the wave.
 //
 // Usage: gemm_tiles_check M N BN CUS
 // Prints: tiles=<count> missing=<n> repeated=<n> max_full=<n> max_edge=<n>
 //         max_load_x100=<100 * max over workgroups of full + edge / 2>
+//         unchecked_outside=<stores> uncovered=<outputs> blocks_not_inside=<waves>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -33,6 +39,32 @@ int main(int argc, char** argv) {
     const int S = t.per_xcd < per_xcd_cus ? t.per_xcd : per_xcd_cus;  // the launch's grid / 8
     std::vector<int> hits((size_t)t.tiles_m * t.tiles_n, 0);
     int max_full = 0, max_edge = 0, max_load = 0, bad = 0;
+    long long unchecked_outside = 0, uncovered = 0, blocks_not_inside = 0;
+    const int wc = bn / 2;
+    auto check_waves = [&](int tm, int tn) {
+        for (int wm = 0; wm < 2; ++wm)
+            for (int wn = 0; wn < 2; ++wn) {
+                const long long row0 = (long long)tm * 256 + wm * 128, col0 = (long long)tn * bn + wn * wc;
+                const WaveExtent e = wave_extent(M, N, row0, col0, wc);
+                if (e.jmax == 4 && e.imax == wc / 32 && !e.inside) ++blocks_not_inside;
+                for (int r = 0; r < 128; ++r)
+                    for (int c = 0; c < wc; ++c) {
+                        const bool valid = row0 + r < M && col0 + c < N;
+                        if (valid && !(r / 32 < e.jmax && c / 32 < e.imax)) ++uncovered;
+                    }
+                if (!e.inside) continue;
+                for (int j = 2; j < 4; ++j)
+                    for (int r = 0; r < 32; ++r)
+                        for (int i = 0; i < wc / 32; ++i)
+                            for (int vq = 0; vq < 4; ++vq)
+                                for (int h = 0; h < 2; ++h)
+                                    for (int x = 0; x < 4; ++x) {
+                                        const long long m = row0 + 32 * j + r;
+                                        const long long n = col0 + 32 * i + 8 * vq + 4 * h + x;
+                                        if (m >= M || n >= N) ++unchecked_outside;
+                                    }
+            }
+    };
     for (int x = 0; x < 8; ++x)
         for (int slot = 0; slot < S; ++slot) {
             int full = 0, edge = 0, tm, tn;
@@ -42,6 +74,7 @@ int main(int argc, char** argv) {
                     break;
                 }
                 ++hits[(size_t)tm * t.tiles_n + tn];
+                check_waves(tm, tn);
                 if (tm < t.tm_full && tn < t.tn_full) ++full;
                 else ++edge;
             }
@@ -55,7 +88,9 @@ int main(int argc, char** argv) {
         missing += h == 0;
         repeated += h > 1;
     }
-    printf("tiles=%zu missing=%d repeated=%d out_of_range=%d max_full=%d max_edge=%d max_load_x100=%d\n",
-           hits.size(), missing, repeated, bad, max_full, max_edge, max_load);
+    printf("tiles=%zu missing=%d repeated=%d out_of_range=%d max_full=%d max_edge=%d max_load_x100=%d "
+           "unchecked_outside=%lld uncovered=%lld blocks_not_inside=%lld\n",
+           hits.size(), missing, repeated, bad, max_full, max_edge, max_load, unchecked_outside, uncovered,
+           blocks_not_inside);
     return 0;
 }
