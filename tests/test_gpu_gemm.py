@@ -82,6 +82,38 @@ def test_linear_fp8_no_bias_and_strided_out(O, dev):
     assert (out[:, 128:] == 3.0).all()
 
 
+@pytest.mark.parametrize("M,K,N,act", [
+    (100, 1024, 256, 1),    # 256 x 192 tiles; the wave of rows 0-127 has 100 rows (four row blocks)
+    (1000, 1280, 640, 0),   # 256 x 192 tiles; the last tile's second row wave has 104 rows
+    (4964, 1024, 4224, 1),  # 256-wide tiles (340); last row tile 100 deep
+    (5092, 1024, 4224, 0),  # 256-wide tiles; last row tile 228 deep, its second row wave 100
+])
+def test_gemm_writes_nothing_past_m_or_n(dev, M, K, N, act):
+    """The persistent GEMM into a buffer with 64 guard rows below M and 8
+    guard columns right of N (row stride N + 8): the M x N block equals the
+    plain call's output and the guards keep their fill. Shapes whose last
+    row tile leaves a wave 97-127 rows: such a wave has four row blocks but
+    is not wholly inside, and its tile-end stores must keep their bounds
+    test (stores past row M faulted the GPU at M = 100 in a build that
+    counted blocks)."""
+    ops, L = pkg_module("ops"), pkg_module("_lib")
+    print(f"case gemm guard band {M}x{K}x{N} act={act}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + N)
+    a = torch.randint(0, 120, (M, K), dtype=torch.uint8, device=dev, generator=g).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (N, K), dtype=torch.uint8, device=dev, generator=g).view(torch.float8_e4m3fn)
+    sa = torch.rand(M, device=dev, generator=g) * 1e-3 + 1e-4
+    sb = torch.rand(N, device=dev, generator=g) * 1e-3 + 1e-4
+    bias = torch.randn(N, device=dev, generator=g).to(torch.bfloat16)
+    ldc = N + 8
+    buf = torch.full((M + 64, ldc), 7.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.load().hn_gemm_fp8_rowcol(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+                                        bias.data_ptr(), buf.data_ptr(), M, N, K, ldc, act,
+                                        torch.cuda.current_stream().cuda_stream), "gemm")
+    ref = ops.gemm_fp8_rowcol(a, b, sa, sb, bias, act)
+    assert torch.equal(buf[:M, :N], ref)
+    assert bool((buf[M:] == 7.0).all()) and bool((buf[:, N:] == 7.0).all())
+
+
 # K >= 7 x 128 takes the persistent kernel that carries half of each tile's
 # epilogue into the next tile's K loop. Cases: the smallest such K and the
 # largest K below it; ragged M and N (edge tiles); more tiles than CUs, so a
