@@ -703,3 +703,50 @@ def test_v_beyond_fp16_range_enters_as_65504(O, dev):
     assert_close_bf16(got, ref, what="V clipped at 65504")
     unclipped = O.attention_reference(qf, kall, vall)
     assert np.abs(unclipped - got).max() > 1.0
+
+
+@pytest.mark.parametrize("B,H,Lq,n_chunks,chunk,cur,holes", [
+    (2, 128, 300, 2, 512, 64, True),    # 8-wave rows 0-255 + split 4-wave rows 256-299, masks, tail
+    (1, 24, 128, 16, 512, 0, False),    # decode style: key splits and the merge kernel
+    (1, 3, 37, 3, 100, 37, False),      # small 4-wave launch with a tail
+])
+def test_attention_writes_nothing_outside_out(dev, B, H, Lq, n_chunks, chunk, cur, holes):
+    """The output written into a view of a larger buffer (64 guard rows past
+    Lq and one guard head per row): the view equals the contiguous result of
+    the same call and every guard element keeps its fill, for each launch
+    shape (8-wave tiles with the split remainder, key splits with the merge,
+    the plain 4-wave launch)."""
+    print(f"case attn guard band B={B} H={H} Lq={Lq} keys={n_chunks}x{chunk} cur={cur}", flush=True)
+    ops, L = pkg_module("ops"), pkg_module("_lib")
+    D = 128
+    cache = _cache_from_chunks(dev, n_chunks, chunk, H, D, 900 + Lq)
+    kv_len = n_chunks * chunk
+    g = torch.Generator(device=dev).manual_seed(Lq + H)
+    q = torch.randn(B, Lq, H, D, device=dev, generator=g).to(torch.bfloat16)
+    k_cur = v_cur = None
+    if cur:
+        k_cur = torch.randn(B, cur, H, D, device=dev, generator=g).to(torch.bfloat16)
+        v_cur = torch.randn(B, cur, H, D, device=dev, generator=g).to(torch.bfloat16)
+    cache_valid = None
+    if holes:
+        cache_valid = torch.rand(B, kv_len, device=dev, generator=g) > 0.1
+    ref = ops.attn_fp8kv(q, cache["k"], cache["v"], cache["k_scale"], cache["v_scale"], kv_len,
+                         k_cur, v_cur, 0, 0, None, cache_valid, None)
+    buf = torch.full((B, Lq + 64, H + 1, D), 5.0, dtype=torch.bfloat16, device=dev)
+    out = buf[:, :Lq, :H, :]
+    kc, vc = cache["k"].expand(B, -1, -1, -1), cache["v"].expand(B, -1, -1, -1)
+    ksc, vsc = cache["k_scale"].expand(B, -1, -1, -1), cache["v_scale"].expand(B, -1, -1, -1)
+    kvb = None if cache_valid is None else cache_valid.to(torch.uint8).contiguous()
+    lib = L.load()
+    ws_bytes = lib.hn_attn_fp8kv_workspace_size(B, Lq, H, D, kv_len, cur)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
+    L.check(lib.hn_attn_fp8kv(
+        L.HN_KV_FP8, q.data_ptr(), L.strides(q), B, Lq, H, D,
+        kc.data_ptr(), vc.data_ptr(), L.strides(kc), ksc.data_ptr(), vsc.data_ptr(), L.strides(ksc),
+        cache["k"].shape[1], kv_len, L.ptr(kvb), 0 if kvb is None else kvb.stride(0),
+        None if not cur else k_cur.data_ptr(), None if not cur else v_cur.data_ptr(),
+        L.strides(k_cur) if cur else None, cur, None, 0, 0, 0, float(D) ** -0.5,
+        out.data_ptr(), L.strides(out), None if ws is None else ws.data_ptr(), ws_bytes,
+        torch.cuda.current_stream().cuda_stream), "hn_attn_fp8kv")
+    assert torch.equal(out, ref)
+    assert bool((buf[:, Lq:] == 5.0).all()) and bool((buf[:, :, H:] == 5.0).all())
