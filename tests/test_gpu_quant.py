@@ -351,3 +351,72 @@ def test_hardware_e4m3_conversion_matches_oracle_over_quantizer_range(O, dev):
     pool.shutdown()
     print(f"[e4m3] {checked} fp32 inputs, hardware conversion == oracle", flush=True)
     assert checked >= 2 * (last + 1)
+
+
+@pytest.mark.parametrize("cols", [640, 3072, 12288])
+def test_quantizers_write_nothing_past_their_outputs(dev, cols):
+    """Each quantizer writes into buffers 16 rows longer than its output (and,
+    for the blockwise scales, one block row longer), pre-filled: the output
+    part equals the op's own result and every guard byte keeps its fill. The
+    narrow (one wave per row), wide (one workgroup per row), fused LayerNorm
+    and blockwise paths."""
+    print(f"case quant guard band cols={cols}", flush=True)
+    ops, L = pkg_module("ops"), pkg_module("_lib")
+    lib = L.load()
+    st = torch.cuda.current_stream().cuda_stream
+    rows = 300
+    g = torch.Generator(device=dev).manual_seed(cols)
+    x = (torch.randn(rows, cols, device=dev, generator=g) * 2).to(torch.bfloat16)
+
+    def guarded(shape, dtype, fill):
+        t = torch.empty(shape, dtype=dtype, device=dev)
+        t.view(torch.uint8).fill_(fill)
+        return t
+
+    # per-token rows
+    q = guarded((rows + 16, cols), torch.uint8, 0xAB)
+    s = guarded((rows + 16,), torch.float32, 0xCD)
+    L.check(lib.hn_quantize_rows_fp8(x.data_ptr(), rows, cols, cols, L.HN_SCALE_CLAMP, 1e-4,
+                                     q.data_ptr(), s.data_ptr(), st), "rows")
+    qr, sr = ops.quantize_rows_fp8(x)
+    assert torch.equal(q[:rows], qr.view(torch.uint8)) and torch.equal(s[:rows], sr)
+    assert bool((q[rows:] == 0xAB).all()) and bool((s[rows:].view(torch.uint8) == 0xCD).all())
+    # fused LayerNorm + modulate (widths up to 8192)
+    if cols <= 8192:
+        sh = (torch.randn(1, cols, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        sc = (torch.randn(1, cols, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        q = guarded((rows + 16, cols), torch.uint8, 0xAB)
+        s = guarded((rows + 16,), torch.float32, 0xCD)
+        L.check(lib.hn_ln_mod_quantize_fp8(x.data_ptr(), rows, cols, rows, sh.data_ptr(), sc.data_ptr(),
+                                           cols, 1e-6, 1e-4, q.data_ptr(), s.data_ptr(), st), "ln")
+        qr, sr = ops.ln_modulate_quantize_fp8(x.view(1, rows, cols), sh, sc, 1e-6)
+        assert torch.equal(q[:rows], qr.view(rows, cols).view(torch.uint8))
+        assert torch.equal(s[:rows], sr.view(rows))
+        assert bool((q[rows:] == 0xAB).all()) and bool((s[rows:].view(torch.uint8) == 0xCD).all())
+    # blockwise 128 x 128 (300 rows: the last block row is 44 deep)
+    nb = (rows + 127) // 128
+    q = guarded((rows + 16, cols), torch.uint8, 0xAB)
+    s = guarded((nb + 1, cols // 128), torch.float32, 0xCD)
+    L.check(lib.hn_quantize_blockwise_fp8(x.data_ptr(), rows, cols, q.data_ptr(), s.data_ptr(), st), "bw")
+    qr, sr = ops.quantize_blockwise_fp8(x)
+    assert torch.equal(q[:rows], qr.view(torch.uint8)) and torch.equal(s[:nb], sr)
+    assert bool((q[rows:] == 0xAB).all()) and bool((s[nb:].view(torch.uint8) == 0xCD).all())
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "int8"])
+def test_kv_write_touches_only_its_slot(dev, fmt):
+    """A write of 30 tokens at start 40 of a 100-token cache (B 2): codes and
+    scales of tokens [0, 40) and [70, 100) keep their fill."""
+    kvc = pkg_module("fp8_kv_cache")
+    make = kvc.make_fp8_kv_block if fmt == "fp8" else kvc.make_int8_kv_block
+    cache = make(2, 100, 3, 128, device=dev)
+    for t in cache.values():
+        t.view(torch.uint8).fill_(0x5A)
+    g = torch.Generator(device=dev).manual_seed(3)
+    k = (torch.randn(2, 30, 3, 128, device=dev, generator=g) * 2).to(torch.bfloat16)
+    v = (torch.randn(2, 30, 3, 128, device=dev, generator=g) * 2).to(torch.bfloat16)
+    kvc.quantize_kv_pair_into(cache, k, v, 40)
+    for name, t in cache.items():
+        b = t.view(torch.uint8)
+        assert bool((b[:, :40] == 0x5A).all()) and bool((b[:, 70:] == 0x5A).all()), name
+        assert not bool((b[:, 40:70] == 0x5A).all()), name
