@@ -114,6 +114,25 @@ def test_gemm_writes_nothing_past_m_or_n(dev, M, K, N, act):
     assert bool((buf[M:] == 7.0).all()) and bool((buf[:, N:] == 7.0).all())
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 256, 512), (129, 384, 1024), (4097, 128, 4096)])
+def test_blockwise_gemm_writes_nothing_past_m(dev, M, N, K):
+    """The blockwise GEMM into a buffer 16 rows longer than its output: the
+    output rows equal the op's own result and the guard rows keep their fill
+    (last row tiles 44, 1 and 1 deep)."""
+    print(f"case blockwise guard band {M}x{N}x{K}", flush=True)
+    ops, L = pkg_module("ops"), pkg_module("_lib")
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator(device=dev).manual_seed(M)
+    qa, sa = pf._quantize_blockwise(torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16))
+    qb, sb = pf._quantize_blockwise(torch.randn(N, K, device=dev, generator=g).to(torch.bfloat16))
+    buf = torch.full((M + 16, N), 9.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.load().hn_gemm_fp8_blockwise(qa.data_ptr(), qb.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+                                           buf.data_ptr(), M, N, K, torch.cuda.current_stream().cuda_stream),
+            "blockwise")
+    ref = ops.gemm_fp8_blockwise(qa, qb, sa, sb)
+    assert torch.equal(buf[:M], ref) and bool((buf[M:] == 9.0).all())
+
+
 # K >= 7 x 128 takes the persistent kernel that carries half of each tile's
 # epilogue into the next tile's K loop. Cases: the smallest such K and the
 # largest K below it; ragged M and N (edge tiles); more tiles than CUs, so a
