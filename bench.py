@@ -108,7 +108,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ar", action="store_true", help="skip the config-5 AR chunk (about 15 s)")
     ap.add_argument("--only", default="all",
-                    choices=["all", "linear", "kv", "attn", "decode", "blockwise", "copy", "ar", "vendor"])
+                    choices=["all", "linear", "kv", "attn", "decode", "blockwise", "copy", "ar", "vendor",
+                             "gemm_phases"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -564,6 +565,8 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
             tf = gemm_flops(m, k, n) / 1e9
             log(f"{m}x{k}x{n}: hn_gemm_fp8_rowcol {ours * 1e3:.1f} us ({tf / ours:.0f} TFLOP/s), "
                 f"hipBLASLt {theirs * 1e3:.1f} us ({tf / theirs:.0f} TFLOP/s), max |diff| {diff.abs().max().item():.3g}")
+    elif args.only == "gemm_phases":
+        bench_gemm_phases(args, torch, ops, dev, g, log)
     elif args.only in ("attn", "decode"):
         lk = ATT_CHUNKS * KV_L
         cache = kvc.make_fp8_kv_block(1, lk, KV_H, KV_D, device=dev)
@@ -579,6 +582,62 @@ def run_only(args, torch, ops, kvc, ca, dev, log):
             q = torch.randn(1, 128, KV_H, KV_D, device=dev, generator=g).to(torch.bfloat16)
             ms = time_loop(lambda: ca.chunk_attention(q, cache, lk), args.steps, args.warmup)
             log(f"decode-style attention (Lq=128) {ms * 1e3:.1f} us")
+
+
+STAMP_SHAPE = (16, 12, 8)   # workgroups x tiles x phases recorded by the stamps library
+STAMP_PHASES = ("steps 0-4, carrying the previous tile's epilogue", "steps 5 .. KT-1", "end-of-loop barrier",
+                "next tile's step-1 loads", "direct epilogue passes", "conversion of the carried rows",
+                "wait for the next tile's step 0 + barrier")
+
+
+def bench_gemm_phases(args, torch, ops, dev, g, log):
+    """Where a persistent-GEMM tile's cycles go: the measurement library
+    libhynomas_fp8_stamps.so (the same kernel, compiled with
+    HN_GEMM_PHASE_STAMPS) records the shader clock (s_memtime) at each phase
+    boundary of workgroups 0-15's first 12 tiles. Per shape: the time per call,
+    then the median cycles of each phase over those workgroups' whole tiles.
+    HN_GEMM_WG_PER_XCD (environment) caps the launch's workgroups per XCD."""
+    import ctypes
+    import numpy as np
+    lib = ctypes.CDLL(str(ROOT / "hy-nomas_amd" / "libhynomas_fp8_stamps.so"))
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    lib.hn_gemm_fp8_rowcol.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, ctypes.c_int, P]
+    lib.hn_gemm_phase_stamps.argtypes = [P, I64, ctypes.c_int]
+    nbytes = int(np.prod(STAMP_SHAPE)) * 8
+    cap = os.environ.get("HN_GEMM_WG_PER_XCD", "all")
+    for (m, n, k, act) in ((NS_M, NS_N, NS_K, 1), (10752, NS_N, NS_K, 0), (8192, 12288, 12288, 0)):
+        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn(n, k, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        qx, sx = ops.quantize_rows_fp8(x)
+        qw, sw = ops.quantize_rows_fp8(w)
+        del x, w
+        bias = torch.zeros(n, device=dev, dtype=torch.bfloat16)
+        out = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def call():
+            rc = lib.hn_gemm_fp8_rowcol(qx.data_ptr(), qw.data_ptr(), sx.data_ptr(), sw.data_ptr(),
+                                        bias.data_ptr(), out.data_ptr(), m, n, k, n, act, stream)
+            if rc:
+                raise RuntimeError(f"stamps GEMM failed ({rc})")
+        ms = time_loop(call, args.steps, args.warmup)
+        if lib.hn_gemm_phase_stamps(None, nbytes, 1):
+            raise RuntimeError("clearing the phase stamps failed")
+        call()
+        torch.cuda.synchronize()
+        st = np.zeros(STAMP_SHAPE, dtype=np.uint64)
+        if lib.hn_gemm_phase_stamps(st.ctypes.data, nbytes, 0):
+            raise RuntimeError("reading the phase stamps failed")
+        st = st.astype(np.int64)
+        whole = (st[:, :, 0] > 0) & (st[:, :, 1] > 0) & (st[:, :, 7] > 0)   # whole tiles stamp phase 1
+        d = np.diff(st, axis=2)[whole]                                      # [tiles, 7] cycles per phase
+        med = np.median(d, axis=0)
+        tot = float(np.median(d.sum(axis=1)))
+        log(f"{m}x{n}x{k} act {act} (workgroups per XCD: {cap}): {ms * 1e3:.1f} us per call; "
+            f"{len(d)} whole tiles, median {tot:.0f} cycles per tile")
+        for name, c in zip(STAMP_PHASES, med):
+            log(f"    {name:44s} {c:8.0f} cycles  {100 * c / tot:5.1f} %")
+        log(f"    per K step: steps 5 .. KT-1 {med[1] / (k // 128 - 5):.0f} cycles, steps 0-4 {med[0] / 5:.0f}")
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"

@@ -61,5 +61,35 @@ def build(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+STAMPS_LIB_PATH = PKG / "libhynomas_fp8_stamps.so"
+STAMPS_SOURCE = "gemm_fp8.hip"
+
+
+def build_stamps(verbose: bool = False) -> Path:
+    """The measurement library libhynomas_fp8_stamps.so: the same objects as
+    libhynomas_fp8.so with the GEMM compiled under HN_GEMM_PHASE_STAMPS (phase
+    stamps of the persistent kernel, a workgroup cap from the environment),
+    for ``bench.py --only gemm_phases``. Nothing in the product loads it.
+    Call after build()."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    src = CSRC / STAMPS_SOURCE
+    obj = OBJ_DIR / "gemm_fp8_stamps.o"
+    res = subprocess.run([HIPCC, *HIP_FLAGS, "-DHN_GEMM_PHASE_STAMPS", "-c", str(src), "-o", str(obj)],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name} (stamps):\n{res.stderr}")
+    objs = [obj] + [OBJ_DIR / (p.stem + ".o") for p in sources() if p.name != STAMPS_SOURCE]
+    tmp = STAMPS_LIB_PATH.with_suffix(".so.tmp")
+    res = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed (stamps):\n{res.stderr}")
+    os.replace(tmp, STAMPS_LIB_PATH)
+    if verbose:
+        print(f"built {STAMPS_LIB_PATH}", file=sys.stderr)
+    return STAMPS_LIB_PATH
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_stamps(verbose=True)

@@ -22,6 +22,7 @@
 // The MFMA's first operand is the weight tile and its second the activation
 // tile, i.e. the wave computes out^T: each lane then holds four consecutive
 // output columns n..n+3 of one row m and stores them as one 8-byte write.
+#include <cstdlib>
 #include <type_traits>
 
 #include "hn_capi_internal.h"
@@ -929,6 +930,14 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
     }
 }
 
+#ifdef HN_GEMM_PHASE_STAMPS
+// Measurement build only (libhynomas_fp8_stamps.so, read by bench.py --only
+// gemm_phases): thread 0 of workgroups 0-15 records the shader clock
+// (s_memtime) at each phase boundary of its first 12 tiles.
+constexpr int STAMP_WGS = 16, STAMP_TILES = 12, STAMP_PHASES = 8;
+__device__ unsigned long long g_stamps[STAMP_WGS][STAMP_TILES][STAMP_PHASES];
+#endif
+
 // WC: columns per wave, 128 (256 x 256 tiles) or 96 (256 x 192 tiles, which
 // take the edge-tile path: no carried epilogue).
 template <int ACT, int WC>
@@ -1139,7 +1148,17 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // step 0: step 1's 16 loads are newer
     __syncthreads();
 
+#ifdef HN_GEMM_PHASE_STAMPS
+    int stamp_tile = 0;
+    auto stamp = [&](int ph) {
+        if (blockIdx.x < STAMP_WGS && threadIdx.x == 0 && stamp_tile < STAMP_TILES)
+            g_stamps[blockIdx.x][stamp_tile][ph] = __builtin_amdgcn_s_memtime();
+    };
+#else
+    auto stamp = [](int) {};
+#endif
     for (;;) {
+        stamp(0);
         int ntm = 0, ntn = 0;
         const bool more = tile_of_slot(p, xcd, slot + stride, stride, ntm, ntn);
         // Slice (0, 0).
@@ -1169,12 +1188,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             step(2, F{}, std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{}, T{}, F{});
             step(3, F{}, std::integral_constant<int, 3>{}, std::integral_constant<int, 1>{}, T{}, F{});
             step(4, F{}, std::integral_constant<int, 4>{}, std::integral_constant<int, 1>{}, T{}, F{});
+            stamp(1);
             static_assert(O_PASSES == 4, "the unrolled epilogue steps assume four passes");
             for (int k = O_PASSES + 1; k < KT - 2; ++k)
                 step(k, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 1>{}, T{}, F{});
             if (more) set_src(ntm, ntn);  // else step 0 of this tile again: harmless, in bounds
             step(KT - 2, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 2>{}, T{}, F{});
             step(KT - 1, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 0>{}, F{}, F{});
+            stamp(2);
         } else {
             if (pending) oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
             step(0, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 3>{}, T{}, T{});
@@ -1186,6 +1207,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         }
         // Every wave is done reading the last step's pair.
         __syncthreads();
+        stamp(3);
         if (more) {
             // The next tile's step 1 into the last step's pair.
             const int pr = pair_of(KT - 1);
@@ -1195,9 +1217,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
         }
+        stamp(4);
         if (cinside) direct_passes<ACT, WC, false>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
         else direct_passes<ACT, WC, true>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
+        stamp(5);
         convert_tile(acc, y, prm, fresh_lane());
+        stamp(6);
         pm0 = cm0;
         pn0 = cn0;
         pending = true;
@@ -1208,6 +1233,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         // The next tile's step 0 landed: step 1's 16 loads are newer.
         asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
         __syncthreads();
+        stamp(7);
+#ifdef HN_GEMM_PHASE_STAMPS
+        ++stamp_tile;
+#endif
     }
     oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
     // The last step's re-load of step 0 (no next tile) may still be landing.
@@ -1264,7 +1293,16 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
             set_tiles(192);
             if (p.per_xcd > per_xcd_cus) set_tiles(gemm::BN);  // would need a second round
         }
-        const dim3 pgrid((unsigned)(8 * (p.per_xcd < per_xcd_cus ? p.per_xcd : per_xcd_cus)));
+        int wg_cap = per_xcd_cus;
+#ifdef HN_GEMM_PHASE_STAMPS
+        // Measurement build: HN_GEMM_WG_PER_XCD caps the workgroups per XCD
+        // (the tile queues adapt; fewer CUs busy, same tiles).
+        if (const char* e = getenv("HN_GEMM_WG_PER_XCD")) {
+            const int v = atoi(e);
+            if (v >= 1 && v < wg_cap) wg_cap = v;
+        }
+#endif
+        const dim3 pgrid((unsigned)(8 * (p.per_xcd < wg_cap ? p.per_xcd : wg_cap)));
         const hipStream_t st = (hipStream_t)stream;
         if (p.bn == 192) {
             if (act == HN_ACT_GELU_TANH)
@@ -1296,3 +1334,16 @@ extern "C" int hn_gemm_fp8_blockwise(const void* a, const void* b, const float* 
     return gemm_launch(gemm::BLOCKWISE, a, b, sa, sb, nullptr, out, M, N, K, N, HN_ACT_NONE,
                        stream, "hn_gemm_fp8_blockwise");
 }
+
+#ifdef HN_GEMM_PHASE_STAMPS
+// Measurement build only: copies the phase stamps (unsigned 64-bit,
+// [16 workgroups][12 tiles][8 phases]) to host, or clears them (clear != 0).
+extern "C" int hn_gemm_phase_stamps(void* host, int64_t bytes, int clear) {
+    static const unsigned long long zeros[gemm::STAMP_WGS][gemm::STAMP_TILES][gemm::STAMP_PHASES] = {};
+    HN_REQUIRE(bytes == (int64_t)sizeof(zeros), HN_E_ARG, "hn_gemm_phase_stamps: wrong size");
+    const hipError_t e = clear ? hipMemcpyToSymbol(HIP_SYMBOL(gemm::g_stamps), zeros, sizeof(zeros))
+                               : hipMemcpyFromSymbol(host, HIP_SYMBOL(gemm::g_stamps), sizeof(zeros));
+    HN_REQUIRE(e == hipSuccess, HN_E_LAUNCH, "hn_gemm_phase_stamps: copy failed");
+    return HN_OK;
+}
+#endif
