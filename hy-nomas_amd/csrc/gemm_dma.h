@@ -1,7 +1,7 @@
-// Operand-load geometry and tile queues of the persistent FP8 GEMM
-// (gemm_rowcol_oe_kernel), shared by the kernel and by the CPU checkers in
-// tests/: the same functions compute every load's offset and every
-// workgroup's tiles in both.
+// Operand-load geometry, tile queues and output-store geometry of the
+// persistent FP8 GEMM (gemm_rowcol_oe_kernel), shared by the kernel and by
+// the CPU checkers in tests/: the same functions compute every load's offset,
+// every workgroup's tiles and every store's offset in both.
 //
 // Each of the 4 waves fills stage rows by its own index: 1 KB load q of wave
 // w covers rows 64 w + 8 q + lane / 8 (q = 0..7), one 16-byte chunk per lane,
@@ -149,13 +149,10 @@ HN_GEMM_HD bool tile_of_slot(const Q& p, int x, int i, int S, int& tm, int& tn) 
 
 // A wave's share of a tile: the 32-column blocks (imax) and 32-row blocks
 // (jmax) that hold any output inside the M x N matrix -- what its MFMAs
-// compute and its bounds-checked stores cover -- and whether its whole
-// 128-row x wc-column sub-tile is inside the matrix (`inside`), which is what
-// lets its direct stores skip the bounds test. jmax = 4 does not imply
-// inside: a wave with 97..127 rows left still has four row blocks.
+// compute. A wave with 97..127 rows left has four row blocks, some of whose
+// rows are past M: its stores rely on the output window below.
 struct WaveExtent {
     int imax, jmax;
-    bool inside;
 };
 
 HN_GEMM_HD WaveExtent wave_extent(int64_t M, int64_t N, int64_t row0, int64_t col0, int wc) {
@@ -163,9 +160,68 @@ HN_GEMM_HD WaveExtent wave_extent(int64_t M, int64_t N, int64_t row0, int64_t co
     WaveExtent e;
     e.jmax = rows >= 128 ? 4 : (rows <= 0 ? 0 : (int)((rows + 31) >> 5));
     e.imax = cols >= wc ? wc / 32 : (cols <= 0 ? 0 : (int)(cols >> 5));
-    e.inside = rows >= 128 && cols >= wc;
     return e;
 }
+
+// ---------------------------------------------------------------------------
+// Output stores of the persistent kernel, also shared with the CPU checker
+// (tests/gemm_tiles_check.cpp walks every store of every wave through these).
+//
+// A wave stores its 128 x wc sub-tile (first row m0w, first column n0w)
+// through a raw buffer "window": base = element (m0w, n0w), size =
+// out_window_bytes. A store's offset is bytes from the base (row * pitch +
+// 2 * column, pitch = 2 ldc); the buffer's range check drops a store whose
+// offset is at or past the size, i.e. every store to a row at or past M (a
+// store never straddles a row, so never the size). The size is zero when no
+// row or no column block is inside. Columns past N: with wc = 128 and N a
+// multiple of 128 a wave's columns are all inside or none (imax 4 or 0);
+// with wc = 96 each store tests its columns against imax (oe_store_on).
+
+HN_GEMM_HD uint32_t mul24(uint32_t a, uint32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __umul24(a, b);
+#else
+    return (uint32_t)((uint64_t)(a & 0xffffffu) * (uint64_t)(b & 0xffffffu));
+#endif
+}
+
+HN_GEMM_HD int64_t out_window_bytes(int64_t M, int64_t ldc, int64_t m0w, int imax) {
+    const int64_t rows = M - m0w;
+    if (rows <= 0 || imax <= 0) return 0;
+    return (rows > 128 ? 128 : rows) * ldc * 2;
+}
+
+// Carried store q (0..3) of pass P (0..3), 16 bytes read back from the
+// staging area: row 32 (P / 2) + 8 q + lane / 8, columns 64 (P % 2) + 8 (lane
+// % 8) + {0..7} of the sub-tile (stored during the next tile's first K steps
+// or, before an edge tile and after the last tile, at once).
+HN_GEMM_HD uint32_t oe_store_off(uint32_t pitch, int lane, int P, int q) {
+    return mul24((uint32_t)(lane >> 3), pitch) + (uint32_t)((lane & 7) << 4) +
+           (uint32_t)(32 * (P >> 1) + 8 * q) * pitch + (uint32_t)(128 * (P & 1));
+}
+
+HN_GEMM_HD bool oe_store_on(int wc, int imax, int P, int lane) {
+    return wc == 128 || 64 * (P & 1) + 8 * (lane & 7) < 32 * imax;
+}
+
+// Row order of the MFMA fragment reads: lane l reads row oe_row(l % 32) of
+// each 32-row block of both operands (bits 2 and 3 exchanged; an involution
+// that maps each aligned group of 16 rows onto itself). The accumulator block
+// then holds, for lane (h = l / 32, r = l % 32), output row oe_row(r) and
+// columns 16 (v / 8) + 8 h + v % 8 for its values v = 0..15: eight
+// consecutive columns per group of 8 values.
+HN_GEMM_HD int oe_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// Direct store (pass P = 4..7, column block i = 2 (P % 2) + ii, half hv), 16
+// bytes straight from the accumulator: row 32 (P / 2) + oe_row(lane % 32),
+// columns 32 i + 16 hv + 8 (lane / 32) + {0..7} of the sub-tile.
+HN_GEMM_HD uint32_t direct_store_off(uint32_t pitch, int lane, int P, int ii, int hv) {
+    const int i = 2 * (P & 1) + ii;
+    return mul24((uint32_t)oe_row(lane & 31), pitch) + (uint32_t)(32 * (P >> 1)) * pitch +
+           (uint32_t)(2 * (32 * i + 16 * hv + 8 * (lane >> 5)));
+}
+
+HN_GEMM_HD bool direct_store_on(int wc, int imax, int i) { return 32 * i < wc && (wc == 128 || i < imax); }
 
 }  // namespace gemm
 }  // namespace hn

@@ -742,6 +742,22 @@ constexpr int O_PASSES = 2 * O_JO;                  // overlapped passes (steps 
 constexpr int O_MIN_KT = O_PASSES + 3;              // + the tail step + the last two steps
 static_assert(O_SMEM <= 160 * 1024, "LDS");
 
+// Output window of one wave's 128 x wc sub-tile (first row m0w, first column
+// n0w): a raw buffer whose range check drops the stores to rows past M (the
+// store geometry and the window's size are gemm_dma.h's, shared with the CPU
+// checker), so the stores carry no per-lane test and no 64-bit address
+// arithmetic. The launcher bounds ldc (<= 2^22) so that 128 rows of pitch fit
+// the 32-bit offsets.
+constexpr int OUT_RSRC_FLAGS = 0x00020000;  // raw (stride 0) buffer, 32-bit dwords
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+HN_DEVICE __amdgpu_buffer_rsrc_t out_window(const Params& p, int64_t m0w, int64_t n0w, int imax) {
+    const int64_t bytes = out_window_bytes(p.M, p.ldc, m0w, imax);
+    uint16_t* const base = bytes > 0 ? p.out + m0w * p.ldc + n0w : p.out;
+    return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, OUT_RSRC_FLAGS);
+}
+
 // The lane id, regenerated in place (v_mbcnt) by a volatile asm: values
 // derived from it are recomputed where used rather than hoisted and held live
 // across the tile loop.
@@ -785,16 +801,21 @@ HN_DEVICE void param_dma(const Params& p, int64_t m0, int64_t n0, int wm, int wn
     }
 }
 
+
 // y[i][j][w] (j < O_JO) = bf16 pair (2 w, 2 w + 1) of block (i, j): columns
-// 32 i + 8 (w / 2) + 4 (lane / 32) + 2 (w % 2) + {0, 1}, row 32 j + lane % 32
-// of the sub-tile.
+// 32 i + 16 (w / 4) + 8 (lane / 32) + 2 (w % 4) + {0, 1}, row 32 j +
+// oe_row(lane % 32) of the sub-tile (the fragment reads' row order, in
+// gemm_dma.h, puts 8 consecutive columns in each 4 words). Value group vq (4 values) covers columns
+// 32 i + oe_cols(vq, h) + {0..3}.
 // Column groups outer, row blocks inner: one group's scales and bias live at a
 // time. The bias area holds zeros when the layer has no bias.
+HN_DEVICE int oe_cols(int vq, int h) { return 16 * (vq >> 1) + 8 * h + 4 * (vq & 1); }
+
 HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], const uint8_t* prm, int lane) {
     const float* const psa = reinterpret_cast<const float*>(prm);
     const float* const psb = reinterpret_cast<const float*>(prm + 512);
     const uint16_t* const pbias = reinterpret_cast<const uint16_t*>(prm + 1024);
-    const int h = lane >> 5, r = lane & 31;
+    const int h = lane >> 5, r = oe_row(lane & 31);
     float sam[O_JO];
 #pragma unroll
     for (int j = 0; j < O_JO; ++j) sam[j] = psa[32 * j + r];
@@ -802,7 +823,7 @@ HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], c
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
-            const int nl = 32 * i + 8 * vq + 4 * h;
+            const int nl = 32 * i + oe_cols(vq, h);
             const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
             const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
             const float bn0 = bf16_bits_to_f32(bb.x & 0xffffu), bn1 = bf16_bits_to_f32(bb.x >> 16);
@@ -820,9 +841,9 @@ HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], c
 }
 
 // Pass P (block row j = P / 2, weight blocks 2 (P % 2) + {0, 1}) covers the
-// 32 carried values x = 16 ii + 4 vq + e of a lane; group g = x / 4 holds 4
-// consecutive columns (one 8-byte staging write; 128-byte staging rows with
-// 16-byte chunk c at position c ^ ((r >> 1) & 7)).
+// 32 carried values x = 16 ii + 8 hv + 4 (vq % 2) + e of a lane; each 8 of
+// them (ii, hv) are 8 consecutive columns, one 16-byte staging write
+// (128-byte staging rows with 16-byte chunk c at position c ^ ((r >> 1) & 7)).
 //
 // oe_act: the activation of value x in place (bf16 in, bf16 out; the even
 // value of a pair is held in glo until the odd one repacks the word).
@@ -835,11 +856,18 @@ HN_DEVICE void oe_act(uint32_t (&y)[4][4][8], float& glo, int P, int x) {
     else w = pack_bf16(glo, gelu_tanh(__uint_as_float(w & 0xffff0000u)));
 }
 
-HN_DEVICE void oe_write(const uint32_t (&y)[4][4][8], uint8_t* stg, int P, int g, int lane) {
-    const int j = P >> 1, ii = g >> 2, vq = g & 3, i = 2 * (P & 1) + ii;
-    const int r = lane & 31, h = lane >> 5, c = 4 * ii + vq;
-    *reinterpret_cast<uint2*>(stg + r * 128 + ((c ^ ((r >> 1) & 7)) << 4) + 8 * h) =
-        make_uint2(y[i][j][2 * vq], y[i][j][2 * vq + 1]);
+// Staging write of half hv (0, 1) of weight block ii of pass P: 16 bytes,
+// columns 32 ii + 16 hv + 8 (lane / 32) + {0..7} of the pass (16-byte chunk
+// c = 4 ii + 2 hv + lane / 32) in staging row oe_row(lane % 32), from the
+// pair words 4 hv .. 4 hv + 3 of block (2 (P % 2) + ii, P / 2).
+HN_DEVICE void oe_stage16(uint8_t* stg, int ii, int hv, int lane, uint4 v) {
+    const int r = oe_row(lane & 31), c = 4 * ii + 2 * hv + (lane >> 5);
+    *reinterpret_cast<uint4*>(stg + r * 128 + ((c ^ ((r >> 1) & 7)) << 4)) = v;
+}
+
+HN_DEVICE void oe_write(const uint32_t (&y)[4][4][8], uint8_t* stg, int P, int ii, int hv, int lane) {
+    const int j = P >> 1, i = 2 * (P & 1) + ii;
+    oe_stage16(stg, ii, hv, lane, make_uint4(y[i][j][4 * hv], y[i][j][4 * hv + 1], y[i][j][4 * hv + 2], y[i][j][4 * hv + 3]));
 }
 
 // Staging read-back q (0..3) of a pass: rows 8 q + lane / 8, 16-byte chunk lane % 8.
@@ -848,49 +876,46 @@ HN_DEVICE uint4 oe_readback(const uint8_t* stg, int q, int lane) {
     return *reinterpret_cast<const uint4*>(stg + rr * 128 + ((c ^ ((rr >> 1) & 7)) << 4));
 }
 
+// Store q of pass P of the pending sub-tile (gemm_dma.h: oe_store_off), through
+// its output window (pimax: its column blocks inside the matrix).
 template <int WC>
-HN_DEVICE void oe_store(const Params& p, int64_t pm0, int64_t pn0, int wm, int wn, int P, int q, const uint4& v,
+HN_DEVICE void oe_store(__amdgpu_buffer_rsrc_t win, int pimax, uint32_t pitch, int P, int q, const uint4& v,
                         int lane) {
-    const int j = P >> 1, ih = P & 1;
-    const int rr = 8 * q + (lane >> 3), c = lane & 7;
-    const int64_t m = pm0 + wm * 128 + 32 * j + rr;
-    const int nl = 64 * ih + 8 * c;  // column within the wave's wc columns
-    const int64_t n = pn0 + wn * WC + nl;
-    if (m < p.M && n < p.N && (WC == 128 || nl < WC)) *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) = v;
+    if (oe_store_on(WC, pimax, P, lane))
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), win,
+                                               (int)oe_store_off(pitch, lane, P, q), 0, 0);
 }
 
 // All eight passes of a pending tile without overlap (before an edge tile and
 // after a workgroup's last tile).
 template <int ACT, int WC>
-HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, int64_t pm0, int64_t pn0,
-                        int wm, int wn, int lane) {
+HN_DEVICE void oe_flush(const Params& p, uint32_t (&y)[4][4][8], uint8_t* stg, __amdgpu_buffer_rsrc_t win,
+                        int pimax, int lane) {
+    const uint32_t pitch = (uint32_t)p.ldc * 2;
 #pragma unroll
     for (int P = 0; P < O_PASSES; ++P) {
         float glo = 0.0f;
 #pragma unroll
         for (int x = 0; x < 32; ++x) oe_act<ACT>(y, glo, P, x);
 #pragma unroll
-        for (int g = 0; g < 8; ++g) oe_write(y, stg, P, g, lane);
+        for (int g = 0; g < 4; ++g) oe_write(y, stg, P, g >> 1, g & 1, lane);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) oe_store<WC>(p, pm0, pn0, wm, wn, P, q, oe_readback(stg, q, lane), lane);
+        for (int q = 0; q < 4; ++q) oe_store<WC>(win, pimax, pitch, P, q, oe_readback(stg, q, lane), lane);
     }
 }
 
 // Passes 2 j, 2 j + 1 for the row blocks j >= O_JO straight from the
-// accumulator (not carried): scale, bias, activation and stores. A lane holds
-// 4 consecutive columns of one row per (block, vq) and stores them as 8
-// bytes, without the LDS staging of the carried passes: the 8 stores of a
-// pass write every byte of its 32 rows' 128-byte lines, which the L2 merges.
-// (Measured with bias + GELU: 387 against 393 us through the staging area.)
-// CHECK: stores only inside the matrix. A wave whose whole sub-tile is
-// inside (WaveExtent::inside) passes false: without the per-store branch the
-// 32 four-value groups are one basic block whose independent chains the
-// compiler interleaves (with it, each group ran alone as a dependent chain of
-// about 60 instructions).
-template <int ACT, int WC, bool CHECK>
-HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm, int64_t m0,
-                             int64_t n0, int wm, int wn, int lane) {
-    const int h = lane >> 5, r = lane & 31;
+// accumulator (not carried): scale, bias, activation and stores. With the
+// fragment reads' row order each 8 values of a lane are 8 consecutive columns
+// of one row, stored as 16 bytes (gemm_dma.h: direct_store_off) without the
+// LDS staging of the carried passes: a store writes 32 bytes of each of 32
+// rows (the two half waves side by side), and the 4 stores of a pass fill its
+// rows' 128-byte lines, which the L2 merges.
+template <int ACT, int WC>
+HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const uint8_t* prm,
+                             __amdgpu_buffer_rsrc_t win, int imax, int lane) {
+    const int h = lane >> 5, r = oe_row(lane & 31);
+    const uint32_t pitch = (uint32_t)p.ldc * 2;
 #pragma unroll
     for (int P = O_PASSES; P < 8; ++P) {
         // Parameters re-read per pass (opaque offset): common loads kept
@@ -903,11 +928,13 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
         const int j = P >> 1, ih = P & 1;
         const float sam = psa[32 * j + r];
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < 2; ++ii) {
+            const int i = 2 * ih + ii;
+            if (32 * i >= WC) continue;  // block past a 96-column wave
+            uint32_t w[8];
 #pragma unroll
             for (int vq = 0; vq < 4; ++vq) {
-                const int i = 2 * ih + ii, nl = 32 * i + 8 * vq + 4 * h;
-                if (32 * i >= WC) continue;  // block past a 96-column wave
+                const int nl = 32 * i + oe_cols(vq, h);
                 const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
                 const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
                 float v[4] = {fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bf16_bits_to_f32(bb.x & 0xffffu)),
@@ -923,10 +950,16 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
                     v[3] = gelu_tanh(__uint_as_float(o.y & 0xffff0000u));
                     o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
                 }
-                const int64_t m = m0 + wm * 128 + 32 * j + r;
-                const int64_t n = n0 + wn * WC + nl;
-                if (!CHECK || (m < p.M && n < p.N)) *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
+                w[2 * vq] = o.x;
+                w[2 * vq + 1] = o.y;
             }
+            if (direct_store_on(WC, imax, i)) {
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{w[0], w[1], w[2], w[3]}, win,
+                                                       (int)direct_store_off(pitch, lane, P, ii, 0), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{w[4], w[5], w[6], w[7]}, win,
+                                                       (int)direct_store_off(pitch, lane, P, ii, 1), 0, 0);
+            }
+        }
     }
 }
 
@@ -993,18 +1026,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     // the wave's wc columns, 4 or 3 in the interior; jmax activation blocks of
     // 32 rows). Wave-uniform. Tiles with every block inside the matrix take
     // the carried path.
-    // cinside: the wave's whole sub-tile is inside (its direct stores go
-    // unchecked).
     int64_t cm0 = 0, cn0 = 0;
     int cimax = 0, cjmax = 0;
-    bool cinside = false;
     auto set_cur = [&](int tm_, int tn_) {
         cm0 = (int64_t)tm_ * BM;
         cn0 = (int64_t)tn_ * TBN;
         const WaveExtent e = wave_extent(p.M, p.N, cm0 + wm * 128, cn0 + wn * WC, WC);
         cimax = e.imax;
         cjmax = e.jmax;
-        cinside = e.inside;
     };
     int par = 0;  // step s of the current tile uses buffer pair (s + par) & 1
     auto pair_of = [&](int s) { return (s + par) & 1; };
@@ -1019,11 +1048,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     f32x16 acc[4][4];
     i32x8 fa[4], fb[4];
     uint32_t y[4][4][8];         // carried rows (j < O_JO) of the pending tile
-    int64_t pm0 = p.M, pn0 = 0;  // pending tile origin (none yet: every store out of range)
+    // Pending tile: its output window and column blocks inside (none yet: an
+    // empty window, every store dropped).
+    __amdgpu_buffer_rsrc_t pwin = out_window(p, p.M, 0, 0);
+    int pimax = 0;
     bool pending = false;
 
     // Fragment reads. A fragment of block row base + 32 q is 16-byte chunks
-    // c0 = 4 kh + 2 (lane / 32) and c0 + 1 of row base + 32 q + lane % 32; the
+    // c0 = 4 kh + 2 (lane / 32) and c0 + 1 of row base + 32 q + oe_row(lane % 32); the
     // swizzle depends only on the lane (32 q and base are multiples of 16), so
     // a lane needs four offsets (kh x chunk), computed per step from a
     // regenerated lane id (hoisted, they would be held live and spilled).
@@ -1032,7 +1064,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     };
     auto rd_lane = [&](int l) {
         RdLane d;
-        const int r = l & 31, c0 = (l >> 5) * 2;
+        const int r = oe_row(l & 31), c0 = (l >> 5) * 2;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -1085,6 +1117,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         const int el = fresh_lane();
         const DmaLane dl = dma_lane(el);
         const RdLane rl = rd_lane(el);
+        const uint32_t pitch = (uint32_t)p.ldc * 2;
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const int i = s >> 2, j = s & 3;
@@ -1107,7 +1140,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             // Read-back of the previous pass (slots 0-3) before this pass's
             // staging writes (slots 3-15), stores two slots after each read.
             if (PASS >= 1 && s < 4) rb[s] = oe_readback(stg, s, el);
-            if (PASS >= 1 && s >= 2 && s < 6) oe_store<WC>(p, pm0, pn0, wm, wn, PASS - 1, s - 2, rb[s - 2], el);
+            if (PASS >= 1 && s >= 2 && s < 6)
+                oe_store<WC>(pwin, pimax, pitch, PASS - 1, s - 2, rb[s - 2], el);
             const int i = s >> 2, j = s & 3;
             if (i < WC / 32 && (!EDGE || (i < cimax && j < cjmax))) acc[i][j] = mfma(fb[i], fa[j], acc[i][j]);
             if (NEXT) roll(s, an, bnx, 0, rl);
@@ -1122,8 +1156,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             if (DMA == 3 && s >= 8 && s < 13) param_dma<WC>(p, cm0, cn0, wm, wn, el, prm_lds, s - 8);
             if (PASS >= 0 && PASS < O_PASSES) {
                 oe_act<ACT>(y, glo, PASS, 16 + s);
-                if (s >= 4 && s < 8) oe_write(y, stg, PASS, s - 4, el);         // groups 0-3 (half 0)
-                if ((s & 3) == 3) oe_write(y, stg, PASS, 4 + (s >> 2), el);     // groups 4-7, when complete
+                if (s == 4 || s == 5) oe_write(y, stg, PASS, 0, s - 4, el);      // block 0 (half 0's values)
+                if ((s & 7) == 7) oe_write(y, stg, PASS, 1, s >> 3, el);         // block 1, each half when complete
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1197,7 +1231,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             step(KT - 1, F{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 0>{}, F{}, F{});
             stamp(2);
         } else {
-            if (pending) oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+            if (pending) oe_flush<ACT, WC>(p, y, stg, pwin, pimax, fresh_lane());
             step(0, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 3>{}, T{}, T{});
             for (int k = 1; k < KT - 2; ++k)
                 step(k, T{}, std::integral_constant<int, -1>{}, std::integral_constant<int, 1>{}, T{}, F{});
@@ -1218,13 +1252,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
             for (int q = 0; q < 8; ++q) dma_b(d, 1, pr, q);
         }
         stamp(4);
-        if (cinside) direct_passes<ACT, WC, false>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
-        else direct_passes<ACT, WC, true>(p, acc, prm, cm0, cn0, wm, wn, fresh_lane());
+        const __amdgpu_buffer_rsrc_t cwin = out_window(p, cm0 + wm * 128, cn0 + wn * WC, cimax);
+        direct_passes<ACT, WC>(p, acc, prm, cwin, cimax, fresh_lane());
         stamp(5);
         convert_tile(acc, y, prm, fresh_lane());
         stamp(6);
-        pm0 = cm0;
-        pn0 = cn0;
+        pwin = cwin;
+        pimax = cimax;
         pending = true;
         if (!more) break;
         par = (KT + par) & 1;
@@ -1238,7 +1272,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
         ++stamp_tile;
 #endif
     }
-    oe_flush<ACT, WC>(p, y, stg, pm0, pn0, wm, wn, fresh_lane());
+    oe_flush<ACT, WC>(p, y, stg, pwin, pimax, fresh_lane());
     // The last step's re-load of step 0 (no next tile) may still be landing.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
@@ -1255,6 +1289,9 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     HN_REQUIRE(N % 128 == 0 && K % 128 == 0, HN_E_ARG, "FP8 GEMM: N and K must be multiples of 128");
     HN_REQUIRE(K <= 128 * gemm::kMaxKT, HN_E_ARG, "FP8 GEMM: K must be <= 32768");
     HN_REQUIRE(ldc >= N && ldc % 8 == 0, HN_E_ARG, "FP8 GEMM: ldc must be >= N and a multiple of 8");
+    // The persistent kernel's output windows address 128 rows of pitch with
+    // 32-bit offsets.
+    HN_REQUIRE(ldc <= (int64_t)1 << 22, HN_E_ARG, "FP8 GEMM: ldc must be <= 4194304");
     HN_REQUIRE(act == HN_ACT_NONE || act == HN_ACT_GELU_TANH, HN_E_ARG, "FP8 GEMM: unknown activation");
     HN_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(out, 16) && aligned(sa, 4) &&
                    aligned(sb, mode == gemm::ROWCOL ? 16 : 4) && aligned(bias, 8),

@@ -130,7 +130,7 @@ int hn_kv_dequantize(int fmt, const void *q, const int64_t *qs, const float *sca
  * a: e4m3 [M, K] row-major; b: e4m3 [N, K] row-major (the nn.Linear weight
  * layout); sa: fp32 [M]; sb: fp32 [N]; bias: bf16 [N] or NULL; out: bf16
  * [M, N] with row stride ldc. fp32 accumulation. K % 128 == 0, N % 128 == 0,
- * a/b/out 16-byte aligned, ldc % 8 == 0.
+ * a/b/out 16-byte aligned, ldc % 8 == 0, N <= ldc <= 2^22.
  * Replaces F.linear(x, linear_weight(m), b) of the DiT block
  * (nomas_compile_prepost.py:45-47,80-87 via int8_stored_bf16_linear.py:82-100)
  * for FP8 weights, and the DeepGEMM per-token GEMM of fp8.py:27-38. */
