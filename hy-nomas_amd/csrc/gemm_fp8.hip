@@ -733,7 +733,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_kernel(Params p) {
 // themselves).
 constexpr int O_BUFS = 4;
 constexpr int O_STAGE = 32 * 128;                   // per wave: 32 rows x 64 bf16
-constexpr int O_PARAMS = 1280;                      // per wave: 128 + 128 floats, 128 bf16
+constexpr int O_PARAMS = 1792;                      // per wave: 128 + 128 floats, 128 bf16, 128 floats
+constexpr int O_BIAS_F32 = 1280;                    // the bias as fp32 (bias_to_f32), in the param area
 constexpr int O_STAGE_BASE = O_BUFS * R_BUF;
 constexpr int O_PARAM_BASE = O_STAGE_BASE + 4 * O_STAGE;
 constexpr int O_SMEM = O_PARAM_BASE + 4 * O_PARAMS;
@@ -778,7 +779,9 @@ HN_DEVICE void dma_4B_sbase(const void* sbase, uint32_t voff, uint32_t lds) {
 
 // Parameter DMA q (0..4) of a wave's sub-tile, 256 bytes each: row scales at
 // [0, 512), column scales at [512, 1024), bias pairs at [1024, 1280). Indices
-// are clamped to the operand's end (in bounds; never used).
+// are clamped to the operand's end (in bounds; never used). bias_to_f32 then
+// widens the bias to fp32 at [1280, 1792), so the epilogue reads 4 biases as
+// one 16-byte load with no per-value conversion.
 template <int WC>
 HN_DEVICE void param_dma(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane, uint32_t lds, int q) {
     if (q < 2) {
@@ -802,6 +805,15 @@ HN_DEVICE void param_dma(const Params& p, int64_t m0, int64_t n0, int wm, int wn
 }
 
 
+// The wave's 128 bf16 biases (2 per lane) widened to fp32 in its param area,
+// from the wave's own LDS (the param DMA has landed: every step after step 0
+// waits for its loads).
+HN_DEVICE void bias_to_f32(uint8_t* prm, int lane) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(prm + 1024 + 4 * lane);
+    *reinterpret_cast<float2*>(prm + O_BIAS_F32 + 8 * lane) =
+        make_float2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
 // y[i][j][w] (j < O_JO) = bf16 pair (2 w, 2 w + 1) of block (i, j): columns
 // 32 i + 16 (w / 4) + 8 (lane / 32) + 2 (w % 4) + {0, 1}, row 32 j +
 // oe_row(lane % 32) of the sub-tile (the fragment reads' row order, in
@@ -814,7 +826,7 @@ HN_DEVICE int oe_cols(int vq, int h) { return 16 * (vq >> 1) + 8 * h + 4 * (vq &
 HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], const uint8_t* prm, int lane) {
     const float* const psa = reinterpret_cast<const float*>(prm);
     const float* const psb = reinterpret_cast<const float*>(prm + 512);
-    const uint16_t* const pbias = reinterpret_cast<const uint16_t*>(prm + 1024);
+    const float* const pbias = reinterpret_cast<const float*>(prm + O_BIAS_F32);
     const int h = lane >> 5, r = oe_row(lane & 31);
     float sam[O_JO];
 #pragma unroll
@@ -825,15 +837,13 @@ HN_DEVICE void convert_tile(const f32x16 (&acc)[4][4], uint32_t (&y)[4][4][8], c
         for (int vq = 0; vq < 4; ++vq) {
             const int nl = 32 * i + oe_cols(vq, h);
             const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
-            const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
-            const float bn0 = bf16_bits_to_f32(bb.x & 0xffffu), bn1 = bf16_bits_to_f32(bb.x >> 16);
-            const float bn2 = bf16_bits_to_f32(bb.y & 0xffffu), bn3 = bf16_bits_to_f32(bb.y >> 16);
+            const float4 bn = *reinterpret_cast<const float4*>(pbias + nl);
 #pragma unroll
             for (int j = 0; j < O_JO; ++j) {
-                const float y0 = fmaf(acc[i][j][4 * vq + 0], sam[j] * sb4.x, bn0);
-                const float y1 = fmaf(acc[i][j][4 * vq + 1], sam[j] * sb4.y, bn1);
-                const float y2 = fmaf(acc[i][j][4 * vq + 2], sam[j] * sb4.z, bn2);
-                const float y3 = fmaf(acc[i][j][4 * vq + 3], sam[j] * sb4.w, bn3);
+                const float y0 = fmaf(acc[i][j][4 * vq + 0], sam[j] * sb4.x, bn.x);
+                const float y1 = fmaf(acc[i][j][4 * vq + 1], sam[j] * sb4.y, bn.y);
+                const float y2 = fmaf(acc[i][j][4 * vq + 2], sam[j] * sb4.z, bn.z);
+                const float y3 = fmaf(acc[i][j][4 * vq + 3], sam[j] * sb4.w, bn.w);
                 y[i][j][2 * vq] = pack_bf16(y0, y1);
                 y[i][j][2 * vq + 1] = pack_bf16(y2, y3);
             }
@@ -924,7 +934,7 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
         asm volatile("" : "+s"(z));
         const float* const psa = reinterpret_cast<const float*>(prm + z);
         const float* const psb = reinterpret_cast<const float*>(prm + z + 512);
-        const uint16_t* const pbias = reinterpret_cast<const uint16_t*>(prm + z + 1024);
+        const float* const pbias = reinterpret_cast<const float*>(prm + z + O_BIAS_F32);
         const int j = P >> 1, ih = P & 1;
         const float sam = psa[32 * j + r];
 #pragma unroll
@@ -936,11 +946,11 @@ HN_DEVICE void direct_passes(const Params& p, const f32x16 (&acc)[4][4], const u
             for (int vq = 0; vq < 4; ++vq) {
                 const int nl = 32 * i + oe_cols(vq, h);
                 const float4 sb4 = *reinterpret_cast<const float4*>(psb + nl);
-                const uint2 bb = *reinterpret_cast<const uint2*>(pbias + nl);
-                float v[4] = {fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bf16_bits_to_f32(bb.x & 0xffffu)),
-                              fmaf(acc[i][j][4 * vq + 1], sam * sb4.y, bf16_bits_to_f32(bb.x >> 16)),
-                              fmaf(acc[i][j][4 * vq + 2], sam * sb4.z, bf16_bits_to_f32(bb.y & 0xffffu)),
-                              fmaf(acc[i][j][4 * vq + 3], sam * sb4.w, bf16_bits_to_f32(bb.y >> 16))};
+                const float4 bn = *reinterpret_cast<const float4*>(pbias + nl);
+                float v[4] = {fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bn.x),
+                              fmaf(acc[i][j][4 * vq + 1], sam * sb4.y, bn.y),
+                              fmaf(acc[i][j][4 * vq + 2], sam * sb4.z, bn.z),
+                              fmaf(acc[i][j][4 * vq + 3], sam * sb4.w, bn.w)};
                 // The activation sees the bf16-rounded linear output, as when carried.
                 uint2 o = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
                 if (ACT == HN_ACT_GELU_TANH) {
@@ -989,7 +999,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     const int KT = (int)(p.K / BK);
     const uint32_t lds_base = lds_addr(smem) + wave * 8 * 1024;
     uint8_t* const stg = smem + O_STAGE_BASE + wave * O_STAGE;
-    const uint8_t* const prm = smem + O_PARAM_BASE + wave * O_PARAMS;
+    uint8_t* const prm = smem + O_PARAM_BASE + wave * O_PARAMS;
     const uint32_t prm_lds = lds_addr(prm);
 
     // DMA source: the tile whose stages are being loaded. A 1 KB load q of
@@ -1154,6 +1164,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
                 else dma_b(dl, 0, dst, s - 8);
             }
             if (DMA == 3 && s >= 8 && s < 13) param_dma<WC>(p, cm0, cn0, wm, wn, el, prm_lds, s - 8);
+            if (DMA == 0 && !NEXT && s == 2) bias_to_f32(prm, el);  // the last step: its slots are free
             if (PASS >= 0 && PASS < O_PASSES) {
                 oe_act<ACT>(y, glo, PASS, 16 + s);
                 if (s == 4 || s == 5) oe_write(y, stg, PASS, 0, s - 4, el);      // block 0 (half 0's values)
