@@ -289,3 +289,89 @@ def test_install_serialized_fp8(O, W, dev):
     bad_scale = dict(state, **{"layers.0.mlp.gate_proj.fp8_scale": -state["layers.0.mlp.gate_proj.fp8_scale"]})
     with pytest.raises(ValueError, match="positive"):
         W.install_serialized_fp8(fresh(), bad_scale, meta)
+
+
+class _Int8Stored(nn.Module):
+    """Stand-in for the reference's Int8StoredBF16Linear
+    (int8_stored_bf16_linear.py:64-89): int8 weight_q, fp32 group scales, bias."""
+
+    def __init__(self, q, s, bias=None):
+        super().__init__()
+        self.register_buffer("weight_q", q)
+        self.register_buffer("weight_scale", s)
+        self.bias = bias
+
+
+class _Int8Model(nn.Module):
+    def __init__(self, t):
+        super().__init__()
+        self.a = _Int8Stored(t["a.weight_q"], t["a.weight_scale"], nn.Parameter(t["a.bias"], requires_grad=False))
+        self.inner = nn.Sequential(_Int8Stored(t["b.weight_q"], t["b.weight_scale"]), nn.LayerNorm(256))
+        # not a multiple of 128: left in place
+        self.odd = _Int8Stored(torch.zeros(100, 256, dtype=torch.int8), torch.ones(100, 2))
+
+
+def test_cache_int8_weights_recognises_only_int8_stored_layers(O):
+    """The installer's resident-weight cache (hy_nomas_quantization.py:43-58)
+    touches nothing in a model without INT8-stored layers."""
+    qz = pkg_module("quantization")
+    plain = nn.Sequential(nn.Linear(128, 128), nn.LayerNorm(128))
+    assert qz.cache_int8_weights(plain) == {}
+    assert isinstance(plain[0], nn.Linear)
+    t = _tensors(O)
+    assert qz._is_int8_stored(_Int8Stored(t["a.weight_q"], t["a.weight_scale"]))
+    assert not qz._is_int8_stored(_Int8Stored(t["a.weight_q"].float(), t["a.weight_scale"]))
+    assert not qz._is_int8_stored(_Int8Stored(t["a.weight_q"], t["a.weight_scale"][:, :1]))
+
+
+def test_install_fp8_reference_call_form(monkeypatch):
+    """install_fp8(source, cutlass, capability) as the reference's call site
+    makes it (hy_nomas_quantization.py:35-40): gfx950's capability patches the
+    reference's cutlass_fp8 module, any other raises ValueError first."""
+    import sys
+    import types
+    from pathlib import Path
+    qz = pkg_module("quantization")
+    with pytest.raises(ValueError, match="gfx950"):
+        qz.install_fp8(Path("/nonexistent/reference"), Path("/nonexistent/cutlass"), (10, 0))
+    with pytest.raises(ValueError, match="gfx950"):
+        qz.install_fp8(Path("/nonexistent/reference"), None, (8, 9))
+    names = ["hymm", "hymm.models", "hymm.models.vae", "hymm.models.vae.pixelumm_decoder",
+             "hymm.models.vae.pixelumm_decoder.cutlass_fp8"]
+    mods = [types.ModuleType(n) for n in names]
+    for parent, child, n in zip(mods, mods[1:], names[1:]):
+        setattr(parent, n.rsplit(".", 1)[1], child)
+    for n, m in zip(names, mods):
+        monkeypatch.setitem(sys.modules, n, m)
+    target = mods[-1]
+    target.load_extension = lambda: "cutlass build"
+    qz.install_fp8(Path("/nonexistent/reference"), None, qz.GFX950)
+    assert type(target.load_extension()).__name__ == "HipFP8Extension"
+
+
+@pytest.mark.gpu
+def test_cache_int8_weights_makes_fp8_resident_layers(O, W, dev):
+    """Every INT8-stored layer becomes an FP8StoredLinear whose codes are the
+    per-channel e4m3 requantization of the reference's bf16 weight (bit-exact
+    with the oracle), with its bias; the forward is the FP8 linear."""
+    print("case cache_int8_weights", flush=True)
+    qz = pkg_module("quantization")
+    dl = pkg_module("dit_fp8_linear")
+    t = _tensors(O)
+    model = _Int8Model({k: v.to(dev) for k, v in t.items()}).to(dev)
+    reports = qz.cache_int8_weights(model)
+    assert sorted(reports) == ["a", "inner.0"]
+    assert isinstance(model.a, dl.FP8StoredLinear) and isinstance(model.inner[0], dl.FP8StoredLinear)
+    assert isinstance(model.odd, _Int8Stored)
+    for name, m in (("a", model.a), ("b", model.inner[0])):
+        w_bits = bf16_bits(W.dequantize_int8_weight(t[name + ".weight_q"], t[name + ".weight_scale"]))
+        qo, so = O.quantize_rows_fp8(w_bits, O.SCALE_CLAMP)
+        assert np.array_equal(u8(m.weight_q), qo) and np.array_equal(m.weight_scale.cpu().numpy(), so)
+    assert reports["a"]["rel_l2"] < 0.05
+    x = torch.randn(40, 256, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y = model.a(x)
+    qx, sx = O.quantize_rows_fp8(bf16_bits(x))
+    ref = O.linear_reference(qx, sx, u8(model.a.weight_q), model.a.weight_scale.cpu().numpy(),
+                             O.bf16_bits_to_f32(bf16_bits(t["a.bias"])))
+    assert_close_bf16(y.float().cpu().numpy(), ref, what="cached INT8 layer as FP8 linear")
