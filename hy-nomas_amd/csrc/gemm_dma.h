@@ -59,6 +59,40 @@ HN_GEMM_HD uint32_t dma_offset(const DmaLane& d, int q, int64_t K, uint32_t lim)
 
 
 // ---------------------------------------------------------------------------
+// Operand loads of the tail-stripe kernel (gemm_tail_kernel), also shared with
+// the CPU checker. A wave's stage holds the stripe's ar = 32 JB A rows, then
+// its workgroup's 32 B rows, 128 bytes of K each; load q of a K step fills
+// stage rows 8 q .. 8 q + 7, lane l bringing row 8 q + l / 8's logical chunk
+// swz_pos(row, l % 8). Its source is A row min(m0 + row, M - 1) (rows past M
+// repeat the last row; their outputs are not stored) or B row n0 + row - ar;
+// tail_src gives the byte offset at K step 0 from that operand's start (a K
+// step adds 128).
+struct TailSrc {
+    bool a;
+    int64_t off;
+};
+
+HN_GEMM_HD TailSrc tail_src(int q, int l, int ar, int64_t m0, int64_t M, int64_t n0, int64_t K) {
+    const int row = 8 * q + (l >> 3);
+    const int64_t chunk = (int64_t)swz_pos(row, l & 7) * 16;
+    TailSrc t;
+    t.a = row < ar;
+    if (t.a) {
+        const int64_t m = m0 + row;
+        t.off = (m < M ? m : M - 1) * K + chunk;
+    } else {
+        t.off = (n0 + row - ar) * K + chunk;
+    }
+    return t;
+}
+
+// K steps of a tail wave: wave w of SK takes steps w + SK t, t < T =
+// tail_steps(KT, w, SK); loads issued past its last step repeat step T - 1
+// (in bounds, never read), so every step issues the same loads.
+HN_GEMM_HD int tail_steps(int KT, int w, int SK) { return (KT - w + SK - 1) / SK; }
+HN_GEMM_HD int tail_step(int w, int SK, int t, int T) { return w + SK * (t < T ? t : T - 1); }
+
+// ---------------------------------------------------------------------------
 // Tile queues of the row/column kernels, also shared with the CPU checker
 // (tests/gemm_tiles_check.cpp enumerates every workgroup's tiles through these
 // functions).

@@ -1288,6 +1288,148 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------
+// The last M % 256 <= TAIL_ROWS rows of a persistent row/column GEMM, [m0, M).
+//
+// As a 256-row tile of the persistent kernel such a stripe keeps the whole K
+// loop of a full tile -- its DMAs, waits and barriers -- for a fraction of the
+// MFMAs, and its K steps wait on their loads' latency: at the north star
+// (M 10 800, 48 tail rows, 48 column tiles) an edge tile took about as long as
+// a full one and the edge tiles put a ninth tile round on some workgroups
+// (10 800 rows 362 us against 10 752 rows 317 us, same box).
+//
+// Here a workgroup owns 32 output columns of the stripe's JB 32-row blocks and
+// splits K over its SK waves: wave w multiplies the 128-byte K steps w,
+// w + SK, w + 2 SK, ... Each wave streams its steps through TAIL_STAGES
+// private LDS stages (the A rows of the stripe, then the 32 B rows), filled
+// by whole-line direct loads (dma_16B, 8 rows per 1 KB load) in the persistent
+// kernel's swizzled row layout and read back as MFMA fragments (read_frag);
+// no barrier is needed until the end. The waves' partial sums meet in LDS and
+// are added in wave order, so the result is deterministic. The epilogue is
+// the persistent kernel's: bf16(acc sa sb + bias), GELU-tanh of that bf16
+// value, rounded to bf16; each thread stores 8 consecutive columns of one row
+// (16 bytes); rows past M are loaded as the last row and not stored.
+constexpr int TAIL_ROWS = 64;
+constexpr int TAIL_COLS = 32;
+constexpr int TAIL_STAGES = 3;
+static_assert(O_MIN_KT >= 4, "every tail wave needs a K step (K / 128 >= O_MIN_KT, at most 4 waves)");
+
+template <int JB>
+constexpr int tail_stage_bytes() { return (32 * JB + 32) * BK; }
+template <int SK, int JB>
+constexpr int tail_smem_bytes() { return SK * TAIL_STAGES * tail_stage_bytes<JB>(); }
+
+template <int ACT, int SK, int JB>
+__global__ __launch_bounds__(64 * SK) void gemm_tail_kernel(Params p, int64_t m0) {
+    constexpr int AR = 32 * JB, NQ = (AR + 32) / 8, STG = tail_stage_bytes<JB>();
+    static_assert(JB * 64 * 16 * 4 <= STG, "a wave's partial sums fit its stages");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[tail_smem_bytes<SK, JB>()];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t n0 = (int64_t)blockIdx.x * TAIL_COLS;
+    const int64_t K = p.K;
+    uint8_t* const ws = smem + w * TAIL_STAGES * STG;
+    const uint32_t ws_lds = lds_addr(ws);
+    // Load q of a step fills stage rows 8 q .. 8 q + 7; lane l brings 16 bytes of
+    // row 8 q + l / 8: the logical chunk that the swizzle puts at physical chunk l % 8.
+    const uint8_t* src[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const TailSrc ts = tail_src(q, lane, AR, m0, p.M, n0, K);
+        src[q] = (ts.a ? p.a : p.b) + ts.off;
+    }
+    const int KT = (int)(K / BK);
+    const int T = tail_steps(KT, w, SK);  // this wave's steps: w + SK t, t < T (T >= 1)
+    // Step t into stage st (tail_step: past the last step, step T - 1 again).
+    auto issue = [&](int st, int t) {
+        const int64_t off = (int64_t)tail_step(w, SK, t, T) * BK;
+        const uint32_t base = ws_lds + st * STG;
+        // The stage's fragment reads have landed before its refill is issued.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) dma_16B(src[q] + off, base + q * 1024);
+    };
+    f32x16 acc[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < TAIL_STAGES; ++d) issue(d, d);
+    int st = 0;
+    for (int t = 0; t < T; ++t) {
+        // Step t's loads are the oldest in flight: (TAIL_STAGES - 1) NQ later ones may stay.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((TAIL_STAGES - 1) * NQ) : "memory");
+        const uint8_t* const sb = ws + st * STG;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const i32x8 fb = read_frag(sb, AR + (lane & 31), kh, lane);
+#pragma unroll
+            for (int j = 0; j < JB; ++j) acc[j] = mfma(fb, read_frag(sb, 32 * j + (lane & 31), kh, lane), acc[j]);
+        }
+        issue(st, t + TAIL_STAGES);
+        st = st + 1 == TAIL_STAGES ? 0 : st + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-loads past the last step
+    float* const part = reinterpret_cast<float*>(ws);  // [(block * 64 + lane) * 16 + register]
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4*>(part + (j * 64 + lane) * 16 + 4 * q) =
+                make_float4(acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]);
+    __syncthreads();
+    // Item it: row ml = it / 4 of the stripe, columns 8 g .. 8 g + 7 (g = it % 4).
+    // acc[j][v] of lane l is out^T for column 8 (v / 4) + 4 (l / 32) + v % 4 and
+    // row 32 j + l % 32, so column 8 g + 4 hh + b is register 4 g + b of lane
+    // ml % 32 + 32 hh.
+    for (int it = threadIdx.x; it < JB * 32 * 4; it += 64 * SK) {
+        const int ml = it >> 2, g = it & 3;
+        const int64_t m = m0 + ml;
+        if (m >= p.M) continue;
+        const int j = ml >> 5, rr = ml & 31;
+        float y[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int ww = 0; ww < SK; ++ww) {
+                const float* const pw = reinterpret_cast<const float*>(smem + ww * TAIL_STAGES * STG);
+                const float4 q = *reinterpret_cast<const float4*>(pw + (j * 64 + rr + 32 * hh) * 16 + 4 * g);
+                s.x += q.x; s.y += q.y; s.z += q.z; s.w += q.w;
+            }
+            y[4 * hh] = s.x; y[4 * hh + 1] = s.y; y[4 * hh + 2] = s.z; y[4 * hh + 3] = s.w;
+        }
+        const int64_t n = n0 + 8 * g;
+        const float sam = p.sa[m];
+        const float4 sb0 = *reinterpret_cast<const float4*>(p.sb + n);
+        const float4 sb1 = *reinterpret_cast<const float4*>(p.sb + n + 4);
+        const float sbv[8] = {sb0.x, sb0.y, sb0.z, sb0.w, sb1.x, sb1.y, sb1.z, sb1.w};
+        float bv[8] = {};
+        if (p.bias) {
+            const uint2 b0 = *reinterpret_cast<const uint2*>(p.bias + n);
+            const uint2 b1 = *reinterpret_cast<const uint2*>(p.bias + n + 4);
+            const uint32_t bw[4] = {b0.x, b0.y, b1.x, b1.y};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                bv[2 * c] = bf16_bits_to_f32(bw[c] & 0xffffu);
+                bv[2 * c + 1] = bf16_bits_to_f32(bw[c] >> 16);
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float v0 = fmaf(y[2 * c], sam * sbv[2 * c], bv[2 * c]);
+            const float v1 = fmaf(y[2 * c + 1], sam * sbv[2 * c + 1], bv[2 * c + 1]);
+            o[c] = pack_bf16(v0, v1);
+            if (ACT == HN_ACT_GELU_TANH)
+                o[c] = pack_bf16(gelu_tanh(__uint_as_float(o[c] << 16)),
+                                 gelu_tanh(__uint_as_float(o[c] & 0xffff0000u)));
+        }
+        *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 }  // namespace gemm
 }  // namespace hn
 
@@ -1310,16 +1452,22 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     if (M == 0) return HN_OK;
     HN_REQUIRE(a && b && sa && sb && out, HN_E_ARG, "FP8 GEMM: null pointer");
     if (const int rc = require_gfx950(who); rc != HN_OK) return rc;
-    gemm::Params p;
+    gemm::Params p{};
     p.a = (const uint8_t*)a; p.b = (const uint8_t*)b;
     p.sa = sa; p.sb = sb;
     p.bias = (const uint16_t*)bias;
     p.out = (uint16_t*)out;
     p.M = M; p.N = N; p.K = K; p.ldc = ldc; p.act = act;
-    const int64_t tm = (M + gemm::BM - 1) / gemm::BM;
-    HN_REQUIRE(tm * ((N + 191) / 192) <= 0x7fffffffLL, HN_E_ARG, "FP8 GEMM: too many tiles");
+    HN_REQUIRE((M + gemm::BM - 1) / gemm::BM * ((N + 191) / 192) <= 0x7fffffffLL, HN_E_ARG,
+               "FP8 GEMM: too many tiles");
+    const bool persistent = mode == gemm::ROWCOL && K / gemm::BK >= gemm::O_MIN_KT;
+    // Persistent launches hand a last row stripe of at most TAIL_ROWS rows to
+    // gemm_tail_kernel and tile only the rows above it.
+    const int64_t m_tail = M % gemm::BM;
+    const int64_t Mt = persistent && m_tail <= gemm::TAIL_ROWS ? M - m_tail : M;
+    const int64_t tm = (Mt + gemm::BM - 1) / gemm::BM;
     auto set_tiles = [&](int bn) {
-        const gemm::TileCounts t = gemm::tile_counts(M, N, bn);
+        const gemm::TileCounts t = gemm::tile_counts(Mt, N, bn);
         p.bn = bn;
         p.tiles_m = t.tiles_m; p.tiles_n = t.tiles_n;
         p.tm_full = t.tm_full; p.tn_full = t.tn_full; p.m_tail = t.m_tail;
@@ -1328,7 +1476,30 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     };
     set_tiles(gemm::BN);
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    if (mode == gemm::ROWCOL && K / gemm::BK >= gemm::O_MIN_KT) {
+    if (persistent && Mt < M) {
+        // The tail stripe first (it only reads the operands), with the full M
+        // for its row clamp and stores. K is split over 2 waves, or 4 when
+        // the stripe has fewer 32-column groups than CUs.
+        gemm::Params pt = p;
+        pt.M = M;
+        const dim3 tgrid((unsigned)(N / gemm::TAIL_COLS));
+        const hipStream_t st = (hipStream_t)stream;
+        const bool two = m_tail > 32, four = N / gemm::TAIL_COLS < device_cus(), gelu = act == HN_ACT_GELU_TANH;
+        const dim3 tblock(four ? 256 : 128);
+#define HN_TAIL(A, SK, JB) gemm::gemm_tail_kernel<A, SK, JB><<<tgrid, tblock, 0, st>>>(pt, Mt)
+        if (gelu) {
+            if (four) { if (two) HN_TAIL(HN_ACT_GELU_TANH, 4, 2); else HN_TAIL(HN_ACT_GELU_TANH, 4, 1); }
+            else { if (two) HN_TAIL(HN_ACT_GELU_TANH, 2, 2); else HN_TAIL(HN_ACT_GELU_TANH, 2, 1); }
+        } else {
+            if (four) { if (two) HN_TAIL(HN_ACT_NONE, 4, 2); else HN_TAIL(HN_ACT_NONE, 4, 1); }
+            else { if (two) HN_TAIL(HN_ACT_NONE, 2, 2); else HN_TAIL(HN_ACT_NONE, 2, 1); }
+        }
+#undef HN_TAIL
+        if (const int rc = check_launch(who); rc != HN_OK) return rc;
+        if (Mt == 0) return HN_OK;
+        p.M = Mt;
+    }
+    if (persistent) {
         // Persistent: per XCD, min(queue length, CUs of the XCD) workgroups.
         // A launch of fewer 256-wide tiles than CUs is one round whatever
         // the tile; 192-wide tiles (three 32-column blocks per wave) do 3/4

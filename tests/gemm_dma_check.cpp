@@ -8,6 +8,15 @@
 //   nocap: leave the offsets uncapped (the checker must then find loads out
 //          of bounds for a shape whose last tile is partial).
 // Prints "loads=<n> out_of_bounds=<n> wrong_offset=<n>"; exit 0.
+//
+// usage: gemm_dma_check tail M N K SK JB
+//   The tail-stripe kernel's loads (tail_src, tail_steps, tail_step) for the
+//   stripe [M - M % 256, M) when M % 256 <= 64, else [0, M) (M <= 64): every
+//   load of every workgroup (N / 32 of them), wave, lane and issued step
+//   (the TAIL_STAGES = 3 re-loads past a wave's last step included), against
+//   its operand's extent; the rows inside the stripe and the B rows at their
+//   exact offsets; and each K step multiplied by exactly one wave.
+// Prints "loads=<n> out_of_bounds=<n> wrong_offset=<n> step_cover_errors=<n>".
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -17,7 +26,51 @@
 
 using namespace hn::gemm;
 
+static int tail_main(int argc, char** argv) {
+    if (argc != 7) {
+        fprintf(stderr, "usage: %s tail M N K SK JB\n", argv[0]);
+        return 2;
+    }
+    const int64_t M = atoll(argv[2]), N = atoll(argv[3]), K = atoll(argv[4]);
+    const int SK = atoi(argv[5]), JB = atoi(argv[6]);
+    if (M <= 0 || N <= 0 || N % 128 || K % 128 || K / 128 < SK || (JB != 1 && JB != 2)) {
+        fprintf(stderr, "bad shape\n");
+        return 2;
+    }
+    const int64_t m0 = M % 256 <= 64 && M >= 256 ? M - M % 256 : 0;
+    const int ar = 32 * JB, nq = (ar + 32) / 8, KT = (int)(K / 128);
+    long long loads = 0, oob = 0, wrong = 0, cover = 0;
+    for (int64_t blk = 0; blk < N / 32; ++blk) {
+        const int64_t n0 = blk * 32;
+        int* hits = (int*)calloc((size_t)KT, sizeof(int));
+        for (int w = 0; w < SK; ++w) {
+            const int T = tail_steps(KT, w, SK);
+            if (T < 1) ++cover;
+            for (int t = 0; t < T; ++t) ++hits[tail_step(w, SK, t, T)];
+            for (int lane = 0; lane < 64; ++lane)
+                for (int q = 0; q < nq; ++q) {
+                    const TailSrc ts = tail_src(q, lane, ar, m0, M, n0, K);
+                    const int row = 8 * q + (lane >> 3);
+                    const int64_t chunk = (int64_t)swz_pos(row, lane & 7) * 16;
+                    if (ts.a && m0 + row < M && ts.off != (m0 + row) * K + chunk) ++wrong;
+                    if (!ts.a && ts.off != (n0 + row - ar) * K + chunk) ++wrong;
+                    const int64_t extent = ts.a ? M : N;
+                    for (int t = 0; t < T + 3; ++t) {
+                        const int64_t addr = ts.off + (int64_t)tail_step(w, SK, t, T) * 128;
+                        ++loads;
+                        if (addr < 0 || addr + 16 > extent * K) ++oob;
+                    }
+                }
+        }
+        for (int s = 0; s < KT; ++s) cover += hits[s] != 1;
+        free(hits);
+    }
+    printf("loads=%lld out_of_bounds=%lld wrong_offset=%lld step_cover_errors=%lld\n", loads, oob, wrong, cover);
+    return 0;
+}
+
 int main(int argc, char** argv) {
+    if (argc > 1 && strcmp(argv[1], "tail") == 0) return tail_main(argc, argv);
     if (argc < 5) {
         fprintf(stderr, "usage: %s M N K bn [nocap]\n", argv[0]);
         return 2;

@@ -43,3 +43,39 @@ def test_the_checker_sees_uncapped_loads(checker):
     # the same loads without the cap: a partial last tile reads past the operand
     r = _run(checker, 132, 3072, 12288, 192, "nocap")
     assert r["out_of_bounds"] > 0 and r["wrong_offset"] == 0, r
+
+
+@pytest.mark.parametrize("M,N,K,SK,JB", [
+    (10800, 12288, 3072, 2, 2), (10800, 3072, 12288, 4, 2), (257, 384, 1024, 2, 1), (288, 640, 896, 4, 1),
+    (289, 512, 3072, 2, 2), (48, 1280, 3072, 4, 2), (1, 256, 4224, 4, 1), (64, 128, 896, 4, 2),
+])
+def test_tail_stripe_loads_stay_inside(checker, M, N, K, SK, JB):
+    """The tail-stripe kernel (the last M % 256 <= 64 rows): every load of
+    every workgroup, wave and issued step -- the re-loads past a wave's last
+    step included -- stays inside its operand, rows inside the stripe keep
+    their exact offsets (rows past M repeat row M - 1), and the split of K
+    over the waves multiplies each K step exactly once."""
+    out = subprocess.run([str(checker), "tail", str(M), str(N), str(K), str(SK), str(JB)], check=True,
+                         capture_output=True, text=True).stdout
+    r = {k: int(v) for k, v in (kv.split("=") for kv in out.split())}
+    assert r["loads"] > 0 and r["out_of_bounds"] == 0 and r["wrong_offset"] == 0, r
+    assert r["step_cover_errors"] == 0, r
+
+
+def test_tail_checker_catches_an_unclamped_row(tmp_path):
+    """Planted in a CPU copy of the header only: without the clamp of A rows
+    past M, the 48-row stripe of M = 10800 (two 32-row blocks) reads past A."""
+    hdr = (HERE.parent / "hy-nomas_amd" / "csrc" / "gemm_dma.h").read_text()
+    planted = hdr.replace("t.off = (m < M ? m : M - 1) * K + chunk;", "t.off = m * K + chunk;")
+    assert planted != hdr
+    (tmp_path / "gemm_dma.h").write_text(planted)
+    src = (HERE / "gemm_dma_check.cpp").read_text().replace('#include "../hy-nomas_amd/csrc/gemm_dma.h"',
+                                                             '#include "gemm_dma.h"')
+    (tmp_path / "check.cpp").write_text(src)
+    exe = tmp_path / "check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Werror", str(tmp_path / "check.cpp"), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe), "tail", "10800", "384", "3072", "2", "2"], check=True, capture_output=True,
+                         text=True).stdout
+    r = {k: int(v) for k, v in (kv.split("=") for kv in out.split())}
+    assert r["out_of_bounds"] > 0, r

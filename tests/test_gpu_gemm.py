@@ -161,6 +161,49 @@ def test_linear_fp8_persistent_tiles(O, dev, M, K, N, gelu, bias):
     _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
 
 
+# A last row stripe of at most 64 rows (M % 256) goes to gemm_tail_kernel
+# (split-K over 4 waves, 8 past K = 4096; one or two 32-row blocks) while the
+# persistent kernel tiles the rows above it; M <= 64 runs the tail kernel
+# alone. Tails of 1, 32, 33, 48 and 64 rows, with and without GELU and bias.
+@pytest.mark.parametrize("M,K,N,gelu,bias", [
+    (257, 1024, 384, True, True),      # 1 tail row: one block, 4 waves
+    (288, 896, 640, False, True),      # 32 tail rows: one block
+    (289, 3072, 512, True, False),     # 33 tail rows: two blocks, no bias
+    (48, 3072, 1280, True, True),      # tail only (no persistent launch)
+    (10800, 12288, 384, False, True),  # 48 tail rows, K 12288: 8 waves
+    (1, 4224, 256, True, True),        # one row, K past 4096
+])
+def test_linear_fp8_tail_rows(O, dev, M, K, N, gelu, bias):
+    print(f"case linear tail {M}x{K}x{N} gelu={gelu} bias={bias}", flush=True)
+    rows = None if M <= 1000 else np.concatenate([np.arange(0, 64), np.arange(M - 320, M)])
+    _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
+
+
+@pytest.mark.parametrize("M,K,N,act", [(300, 1024, 384, 1), (289, 4352, 256, 0), (33, 896, 128, 1)])
+def test_gemm_tail_writes_nothing_past_m_or_n(dev, M, K, N, act):
+    """Tail stripes (44, 33 and 33 rows; the last two on 8 and 4 waves) into a
+    buffer with 64 guard rows and 8 guard columns (row stride N + 8): the
+    M x N block equals the plain call's output, the guards keep their fill,
+    and a second call gives the same bits (the wave-ordered split-K sum)."""
+    ops, L = pkg_module("ops"), pkg_module("_lib")
+    print(f"case gemm tail guard band {M}x{K}x{N} act={act}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + K)
+    a = torch.randint(0, 120, (M, K), dtype=torch.uint8, device=dev, generator=g).view(torch.float8_e4m3fn)
+    b = torch.randint(0, 120, (N, K), dtype=torch.uint8, device=dev, generator=g).view(torch.float8_e4m3fn)
+    sa = torch.rand(M, device=dev, generator=g) * 1e-3 + 1e-4
+    sb = torch.rand(N, device=dev, generator=g) * 1e-3 + 1e-4
+    bias = torch.randn(N, device=dev, generator=g).to(torch.bfloat16)
+    ldc = N + 8
+    buf = torch.full((M + 64, ldc), 7.0, dtype=torch.bfloat16, device=dev)
+    L.check(L.load().hn_gemm_fp8_rowcol(a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+                                        bias.data_ptr(), buf.data_ptr(), M, N, K, ldc, act,
+                                        torch.cuda.current_stream().cuda_stream), "gemm")
+    ref = ops.gemm_fp8_rowcol(a, b, sa, sb, bias, act)
+    assert torch.equal(buf[:M, :N], ref)
+    assert bool((buf[M:] == 7.0).all()) and bool((buf[:, N:] == 7.0).all())
+    assert torch.equal(ops.gemm_fp8_rowcol(a, b, sa, sb, bias, act), ref)
+
+
 @pytest.mark.parametrize("N", [384, 640])
 def test_gemm_rowcol_persistent_strided_out(dev, N):
     """ldc > N on the carried-epilogue path (K = 1024): columns past N untouched.
