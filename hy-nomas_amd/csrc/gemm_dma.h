@@ -86,6 +86,26 @@ HN_GEMM_HD TailSrc tail_src(int q, int l, int ar, int64_t m0, int64_t M, int64_t
     return t;
 }
 
+// The wide form (tail_wide, run by a persistent launch's light workgroups):
+// the stage holds the stripe's ar A rows, then B rows n0 .. n0 + nb - 1 for
+// the workgroup's columns, rows past its last column nlast reading column
+// nlast (never stored); otherwise as tail_src.
+HN_GEMM_HD TailSrc tail_wide_src(int q, int l, int ar, int64_t m0, int64_t M, int64_t n0, int64_t nlast,
+                                 int64_t K) {
+    const int row = 8 * q + (l >> 3);
+    const int64_t chunk = (int64_t)swz_pos(row, l & 7) * 16;
+    TailSrc t;
+    t.a = row < ar;
+    if (t.a) {
+        const int64_t m = m0 + row;
+        t.off = (m < M ? m : M - 1) * K + chunk;
+    } else {
+        const int64_t n = n0 + row - ar;
+        t.off = (n < nlast ? n : nlast) * K + chunk;
+    }
+    return t;
+}
+
 // K steps of a tail wave: wave w of SK takes steps w + SK t, t < T =
 // tail_steps(KT, w, SK); loads issued past its last step repeat step T - 1
 // (in bounds, never read), so every step issues the same loads.
@@ -179,6 +199,34 @@ HN_GEMM_HD bool tile_of_slot(const Q& p, int x, int i, int S, int& tm, int& tn) 
     const int q = (k - fx / S) * L + (s - r);  // this light workgroup's edge tile
     if (q >= px) return false;
     return tile_at(p, x, fx + q, tm, tn);
+}
+
+// A persistent launch without edge tiles can hand the tail stripe (the last
+// M % 256 <= 64 rows) to its "light" workgroups: those with one full tile
+// fewer, idle for the launch's last tile round. light_index numbers them
+// across the XCDs (XCD by XCD, in slot order), -1 for the others;
+// light_count is their number and says whether every XCD has some.
+template <class Q>
+HN_GEMM_HD int light_index(const Q& p, int x, int s, int S) {
+    int before = 0;
+    for (int xx = 0; xx < 8; ++xx) {
+        const int r = (p.tiles_full / 8 + (xx < p.tiles_full % 8 ? 1 : 0)) % S;
+        if (xx == x) return r > 0 && s >= r ? before + (s - r) : -1;
+        before += r > 0 ? S - r : 0;
+    }
+    return -1;
+}
+
+template <class Q>
+HN_GEMM_HD int light_count(const Q& p, int S, bool* every_xcd) {
+    int n = 0;
+    *every_xcd = true;
+    for (int x = 0; x < 8; ++x) {
+        const int r = (p.tiles_full / 8 + (x < p.tiles_full % 8 ? 1 : 0)) % S;
+        if (r == 0) *every_xcd = false;
+        else n += S - r;
+    }
+    return n;
 }
 
 // A wave's share of a tile: the 32-column blocks (imax) and 32-row blocks

@@ -65,6 +65,11 @@ struct Params {
     // which takes 192 when a launch has fewer 256-wide tiles than CUs and
     // more, still at most one per CU, at 192 (its WC template argument).
     int bn;
+    // Persistent kernel: rows [M, tail_M) (tail_M > M only when the tail
+    // stripe rides on the light workgroups, tail_wide) in items of tail_cols
+    // columns, item i for light workgroup i.
+    int64_t tail_M;
+    int tail_cols;
 };
 
 // 16-byte chunk c of LDS row r lives at chunk position c ^ ((r >> 1) & 7).
@@ -981,6 +986,127 @@ constexpr int STAMP_WGS = 16, STAMP_TILES = 12, STAMP_PHASES = 8;
 __device__ unsigned long long g_stamps[STAMP_WGS][STAMP_TILES][STAMP_PHASES];
 #endif
 
+// The tail stripe's columns [n0, n0 + ncols) (ncols <= TAIL_WIDE_COLS, a
+// multiple of 32) over the whole K, by one 4-wave workgroup of the persistent
+// kernel after its last tile: the "light" workgroups (one full tile fewer than
+// the rest, see light_index) run one such item each in the launch's last tile
+// round, where they would otherwise sit idle, instead of a launch of its own
+// for the stripe. Wave w owns columns 96 w .. 96 w + 95 (three 32-column
+// blocks) of the JB row blocks. Each K step's stage -- the stripe's A rows,
+// then the item's B rows -- is filled by the four waves' whole-line direct
+// loads (8 rows per 1 KB load, load q by wave q % 4; tail_wide_src) and
+// shared; two stages, with one barrier after a step's loads land and one after
+// every wave has read its fragments, before that stage is refilled. The
+// epilogue is the persistent kernel's, 8 bytes (4 columns) per store.
+constexpr int TAIL_WIDE_COLS = 384;
+// Where the fused stripe gains (same-box A/B against the separate launch, two
+// runs): the north star (32 light workgroups, K 3072) 0.978x and 0.981x, QKV
+// (24, N 9216) 0.989x and 0.986x. Where it does not: past K 4096 an item
+// outlasts the light workgroups' idle round (fc2, K 12 288: 1.013x), and with
+// 8 light workgroups (out-projection, N 3072) it measured 0.991x and 1.017x.
+constexpr int64_t TAIL_WIDE_MAX_K = 4096;
+constexpr int TAIL_WIDE_MIN_LIGHT = 16;
+
+template <int JB>
+constexpr int tail_wide_stage_bytes() { return (32 * JB + TAIL_WIDE_COLS) * BK; }
+
+template <int ACT, int JB>
+HN_DEVICE void tail_wide(const Params& p, int64_t m0, int64_t M, int64_t n0, int ncols, uint8_t* smem) {
+    constexpr int AR = 32 * JB, NQ = (AR + TAIL_WIDE_COLS) / 8, QW = NQ / 4, STG = tail_wide_stage_bytes<JB>();
+    static_assert(NQ % 4 == 0, "the stage's loads split evenly over the four waves");
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t K = p.K;
+    const uint32_t s_lds = lds_addr(smem);
+    const uint8_t* src[QW];
+#pragma unroll
+    for (int k = 0; k < QW; ++k) {
+        const TailSrc ts = tail_wide_src(w + 4 * k, lane, AR, m0, M, n0, n0 + ncols - 1, K);
+        src[k] = (ts.a ? p.a : p.b) + ts.off;
+    }
+    const int KT = (int)(K / BK);  // >= O_MIN_KT >= 2
+    auto issue = [&](int st, int t) {
+        const int64_t off = (int64_t)t * BK;
+        const uint32_t base = s_lds + st * STG;
+#pragma unroll
+        for (int k = 0; k < QW; ++k) dma_16B(src[k] + off, base + (w + 4 * k) * 1024);
+    };
+    int nb = (ncols - 96 * w) / 32;  // the wave's column blocks inside the item (wave-uniform)
+    nb = nb < 0 ? 0 : (nb > 3 ? 3 : nb);
+    f32x16 acc[3][JB];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < JB; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    issue(0, 0);
+    issue(1, 1);
+    for (int t = 0; t < KT; ++t) {
+        const int st = t & 1;
+        // Step t's loads are the older of at most two steps in flight.
+        if (t + 1 < KT) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(QW) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave's loads of step t have landed
+        const uint8_t* const sb = smem + st * STG;
+        i32x8 fa[2][JB], fb[2][3];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+            for (int j = 0; j < JB; ++j) fa[kh][j] = read_frag(sb, 32 * j + (lane & 31), kh, lane);
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+                if (i < nb) fb[kh][i] = read_frag(sb, AR + 96 * w + 32 * i + (lane & 31), kh, lane);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave has read stage st
+        if (t + 2 < KT) issue(st, t + 2);
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int i = 0; i < 3; ++i)
+                if (i < nb)
+#pragma unroll
+                    for (int j = 0; j < JB; ++j) acc[i][j] = mfma(fb[kh][i], fa[kh][j], acc[i][j]);
+    }
+    // acc[i][j][v] of lane l is out^T for column 96 w + 32 i + 8 (v / 4) + 4 (l / 32) + v % 4
+    // and row 32 j + l % 32 of the item.
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int64_t m = m0 + 32 * j + (lane & 31);
+        if (m >= M) continue;
+        const float sam = p.sa[m];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            if (i >= nb) continue;
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+                const int64_t n = n0 + 96 * w + 32 * i + 8 * vq + 4 * (lane >> 5);
+                const float4 sb4 = *reinterpret_cast<const float4*>(p.sb + n);
+                float bn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (p.bias) {
+                    const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + n);
+                    bn[0] = bf16_bits_to_f32(bb.x & 0xffffu);
+                    bn[1] = bf16_bits_to_f32(bb.x >> 16);
+                    bn[2] = bf16_bits_to_f32(bb.y & 0xffffu);
+                    bn[3] = bf16_bits_to_f32(bb.y >> 16);
+                }
+                const float v0 = fmaf(acc[i][j][4 * vq + 0], sam * sb4.x, bn[0]);
+                const float v1 = fmaf(acc[i][j][4 * vq + 1], sam * sb4.y, bn[1]);
+                const float v2 = fmaf(acc[i][j][4 * vq + 2], sam * sb4.z, bn[2]);
+                const float v3 = fmaf(acc[i][j][4 * vq + 3], sam * sb4.w, bn[3]);
+                uint2 o = make_uint2(pack_bf16(v0, v1), pack_bf16(v2, v3));
+                if (ACT == HN_ACT_GELU_TANH)
+                    o = make_uint2(pack_bf16(gelu_tanh(__uint_as_float(o.x << 16)),
+                                             gelu_tanh(__uint_as_float(o.x & 0xffff0000u))),
+                                   pack_bf16(gelu_tanh(__uint_as_float(o.y << 16)),
+                                             gelu_tanh(__uint_as_float(o.y & 0xffff0000u))));
+                *reinterpret_cast<uint2*>(p.out + m * p.ldc + n) = o;
+            }
+        }
+    }
+}
+
 // WC: columns per wave, 128 (256 x 256 tiles) or 96 (256 x 192 tiles, which
 // take the edge-tile path: no carried epilogue).
 template <int ACT, int WC>
@@ -1286,6 +1412,15 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
     oe_flush<ACT, WC>(p, y, stg, pwin, pimax, fresh_lane());
     // The last step's re-load of step 0 (no next tile) may still be landing.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (p.tail_M > p.M) {
+        const int li = light_index(p, xcd, (int)(blockIdx.x >> 3), stride);
+        const int64_t n0 = (int64_t)li * p.tail_cols;
+        if (li < 0 || n0 >= p.N) return;
+        __syncthreads();  // every wave is past the LDS of its last tile
+        const int nc = (int)(p.N - n0 < p.tail_cols ? p.N - n0 : p.tail_cols);
+        if (p.tail_M - p.M > 32) tail_wide<ACT, 2>(p, p.M, p.tail_M, n0, nc, smem);
+        else tail_wide<ACT, 1>(p, p.M, p.tail_M, n0, nc, smem);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1476,12 +1611,13 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     };
     set_tiles(gemm::BN);
     const dim3 grid((unsigned)(8 * (int64_t)p.per_xcd));
-    if (persistent && Mt < M) {
-        // The tail stripe first (it only reads the operands), with the full M
-        // for its row clamp and stores. K is split over 2 waves, or 4 when
-        // the stripe has fewer 32-column groups than CUs.
+    // The tail stripe on a launch of its own, with the full M for its row
+    // clamp and stores. K is split over 2 waves, or 4 when the stripe has
+    // fewer 32-column groups than CUs.
+    auto launch_tail = [&]() {
         gemm::Params pt = p;
         pt.M = M;
+        pt.tail_M = 0;
         const dim3 tgrid((unsigned)(N / gemm::TAIL_COLS));
         const hipStream_t st = (hipStream_t)stream;
         const bool two = m_tail > 32, four = N / gemm::TAIL_COLS < device_cus(), gelu = act == HN_ACT_GELU_TANH;
@@ -1495,10 +1631,11 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
             else { if (two) HN_TAIL(HN_ACT_NONE, 2, 2); else HN_TAIL(HN_ACT_NONE, 2, 1); }
         }
 #undef HN_TAIL
-        if (const int rc = check_launch(who); rc != HN_OK) return rc;
-        if (Mt == 0) return HN_OK;
-        p.M = Mt;
-    }
+        return check_launch(who);
+    };
+    if (persistent && Mt == 0) return launch_tail();
+    p.M = Mt;
+    p.tail_M = Mt;
     if (persistent) {
         // Persistent: per XCD, min(queue length, CUs of the XCD) workgroups.
         // A launch of fewer 256-wide tiles than CUs is one round whatever
@@ -1521,8 +1658,26 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
             if (v >= 1 && v < wg_cap) wg_cap = v;
         }
 #endif
-        const dim3 pgrid((unsigned)(8 * (p.per_xcd < wg_cap ? p.per_xcd : wg_cap)));
+        const int S = p.per_xcd < wg_cap ? p.per_xcd : wg_cap;
+        const dim3 pgrid((unsigned)(8 * S));
         const hipStream_t st = (hipStream_t)stream;
+        if (Mt < M) {
+            // The tail stripe rides on the light workgroups (tail_wide) when
+            // every XCD has some, at least TAIL_WIDE_MIN_LIGHT in all, there
+            // are no edge tiles, each light workgroup's share of the columns
+            // fits one item and K is at most TAIL_WIDE_MAX_K; else it has a
+            // launch of its own.
+            bool every = false;
+            const int nl = gemm::light_count(p, S, &every);
+            const int64_t cols = nl > 0 ? (N / 32 + nl - 1) / nl * 32 : 0;
+            if (p.tiles_part == 0 && every && nl >= gemm::TAIL_WIDE_MIN_LIGHT && cols <= gemm::TAIL_WIDE_COLS &&
+                K <= gemm::TAIL_WIDE_MAX_K) {
+                p.tail_M = M;
+                p.tail_cols = (int)cols;
+            } else if (const int rc = launch_tail(); rc != HN_OK) {
+                return rc;
+            }
+        }
         if (p.bn == 192) {
             if (act == HN_ACT_GELU_TANH)
                 gemm::gemm_rowcol_oe_kernel<HN_ACT_GELU_TANH, 96><<<pgrid, gemm::NT, 0, st>>>(p);

@@ -17,6 +17,18 @@
 //   its operand's extent; the rows inside the stripe and the B rows at their
 //   exact offsets; and each K step multiplied by exactly one wave.
 // Prints "loads=<n> out_of_bounds=<n> wrong_offset=<n> step_cover_errors=<n>".
+//
+// usage: gemm_dma_check tailwide M N K CUS
+//   The wide tail items the persistent kernel's light workgroups run
+//   (tail_wide_src, light_index, light_count) for a launch over the rows
+//   above the stripe [M - M % 256, M), with CUS / 8 workgroups per XCD (as
+//   the launch takes them): every load of every light workgroup, wave, lane
+//   and K step against its operand, the exact offsets of rows inside the
+//   stripe and of B rows inside the item, the items covering [0, N) exactly
+//   once, and each item on a workgroup with one full tile fewer than the
+//   longest queue. fused=0 when the launch would not fuse the stripe.
+// Prints "fused=<0|1> loads=<n> out_of_bounds=<n> wrong_offset=<n> column_cover_errors=<n>
+//         not_light=<n> cols=<n>".
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -69,8 +81,80 @@ static int tail_main(int argc, char** argv) {
     return 0;
 }
 
+struct Queue {
+    int tiles_n, tm_full, tn_full, tiles_full, tiles_part, m_tail;
+};
+
+static int tailwide_main(int argc, char** argv) {
+    if (argc != 6) {
+        fprintf(stderr, "usage: %s tailwide M N K CUS\n", argv[0]);
+        return 2;
+    }
+    const int64_t M = atoll(argv[2]), N = atoll(argv[3]), K = atoll(argv[4]);
+    const int cus = atoi(argv[5]);
+    if (M <= 0 || N <= 0 || N % 128 || K % 128 || K / 128 < 2 || M % 256 == 0 || M % 256 > 64 || M < 256) {
+        fprintf(stderr, "bad shape\n");
+        return 2;
+    }
+    const int64_t Mt = M - M % 256;
+    const TileCounts t = tile_counts(Mt, N, 256);
+    const Queue q{t.tiles_n, t.tm_full, t.tn_full, t.tiles_full, t.tiles_part, t.m_tail};
+    const int per_xcd_cus = cus / 8 > 0 ? cus / 8 : 1;
+    const int S = t.per_xcd < per_xcd_cus ? t.per_xcd : per_xcd_cus;
+    bool every = false;
+    const int nl = light_count(q, S, &every);
+    const int64_t cols = nl > 0 ? (N / 32 + nl - 1) / nl * 32 : 0;
+    const bool fused = t.tiles_part == 0 && every && nl >= 16 && cols <= 384 && K <= 4096;
+    long long loads = 0, oob = 0, wrong = 0, cover = 0, not_light = 0;
+    if (fused) {
+        const int ar = M % 256 > 32 ? 64 : 32, nq = (ar + 384) / 8, KT = (int)(K / 128);
+        int* hits = (int*)calloc((size_t)N, sizeof(int));
+        int longest = 0;
+        for (int x = 0; x < 8; ++x)
+            for (int s = 0; s < S; ++s) {
+                int n = 0, tm, tn;
+                for (int i = s; tile_of_slot(q, x, i, S, tm, tn); i += S) ++n;
+                longest = n > longest ? n : longest;
+            }
+        for (int x = 0; x < 8; ++x)
+            for (int s = 0; s < S; ++s) {
+                const int li = light_index(q, x, s, S);
+                if (li < 0) continue;
+                int n = 0, tm, tn;
+                for (int i = s; tile_of_slot(q, x, i, S, tm, tn); i += S) ++n;
+                if (n != longest - 1) ++not_light;
+                const int64_t n0 = (int64_t)li * cols;
+                if (n0 >= N) continue;
+                const int64_t nc = N - n0 < cols ? N - n0 : cols;
+                for (int64_t c = n0; c < n0 + nc; ++c) ++hits[c];
+                for (int w = 0; w < 4; ++w)
+                    for (int lane = 0; lane < 64; ++lane)
+                        for (int k = 0; k < nq / 4; ++k) {
+                            const int qq = w + 4 * k;
+                            const TailSrc ts = tail_wide_src(qq, lane, ar, Mt, M, n0, n0 + nc - 1, K);
+                            const int row = 8 * qq + (lane >> 3);
+                            const int64_t chunk = (int64_t)swz_pos(row, lane & 7) * 16;
+                            if (ts.a && Mt + row < M && ts.off != (Mt + row) * K + chunk) ++wrong;
+                            if (!ts.a && row - ar < nc && ts.off != (n0 + row - ar) * K + chunk) ++wrong;
+                            const int64_t extent = ts.a ? M : N;
+                            for (int st = 0; st < KT; ++st) {
+                                const int64_t addr = ts.off + (int64_t)st * 128;
+                                ++loads;
+                                if (addr < 0 || addr + 16 > extent * K) ++oob;
+                            }
+                        }
+            }
+        for (int64_t c = 0; c < N; ++c) cover += hits[c] != 1;
+        free(hits);
+    }
+    printf("fused=%d loads=%lld out_of_bounds=%lld wrong_offset=%lld column_cover_errors=%lld not_light=%lld "
+           "cols=%lld\n", fused ? 1 : 0, loads, oob, wrong, cover, not_light, (long long)cols);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc > 1 && strcmp(argv[1], "tail") == 0) return tail_main(argc, argv);
+    if (argc > 1 && strcmp(argv[1], "tailwide") == 0) return tailwide_main(argc, argv);
     if (argc < 5) {
         fprintf(stderr, "usage: %s M N K bn [nocap]\n", argv[0]);
         return 2;

@@ -79,3 +79,28 @@ def test_tail_checker_catches_an_unclamped_row(tmp_path):
                          text=True).stdout
     r = {k: int(v) for k, v in (kv.split("=") for kv in out.split())}
     assert r["out_of_bounds"] > 0, r
+
+
+@pytest.mark.parametrize("M,N,K,cus,fused", [
+    (10800, 12288, 3072, 256, 1),   # north star: 32 light workgroups, 384 columns each
+    (10800, 9216, 3072, 256, 1),    # QKV: 24 light workgroups
+    (10800, 3072, 12288, 256, 0),   # fc2 (K past 4096): the stripe keeps its own launch
+    (10800, 3072, 3072, 256, 0),    # out-projection: 8 light workgroups, fewer than 16
+    (10800, 4096, 4096, 256, 1),    # 12 light workgroups per XCD, 96 in all, K 4096
+    (10800, 12288, 3072, 80, 1), (300, 384, 1024, 256, 0), (10752 + 33, 4096, 896, 256, 1),
+    (10770, 2048, 1024, 256, 1),
+    (10800, 12288 + 128, 3072, 256, 0),  # a column edge stripe: the stripe keeps its own launch
+])
+def test_tail_items_on_light_workgroups(checker, M, N, K, cus, fused):
+    """The wide tail items the persistent kernel's light workgroups run after
+    their last tile: every load in bounds, the stripe's rows and the item's B
+    rows at their exact offsets, the items covering every column once, and
+    every item on a workgroup with one full tile fewer than the longest
+    queue."""
+    out = subprocess.run([str(checker), "tailwide", str(M), str(N), str(K), str(cus)], check=True,
+                         capture_output=True, text=True).stdout
+    r = {k: int(v) for k, v in (kv.split("=") for kv in out.split())}
+    assert r["fused"] == fused, r
+    if fused:
+        assert r["loads"] > 0 and r["out_of_bounds"] == 0 and r["wrong_offset"] == 0, r
+        assert r["column_cover_errors"] == 0 and r["not_light"] == 0 and r["cols"] <= 384, r

@@ -179,7 +179,23 @@ def test_linear_fp8_tail_rows(O, dev, M, K, N, gelu, bias):
     _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
 
 
-@pytest.mark.parametrize("M,K,N,act", [(300, 1024, 384, 1), (289, 4352, 256, 0), (33, 896, 128, 1)])
+# When every XCD has "light" workgroups (one full tile fewer) and the launch
+# has no edge tiles, the persistent kernel's light workgroups compute the tail
+# stripe themselves after their last tile (tail_wide: up to 384 columns each,
+# the four waves sharing the stripe's A rows), instead of a second launch:
+# the north-star shapes (M 10800) and these.
+@pytest.mark.parametrize("M,K,N,gelu,bias", [
+    (10785, 896, 4096, True, True),    # 33 tail rows (two blocks), 96 light workgroups of 64 columns
+    (10770, 1024, 2048, False, False),  # 18 tail rows (one block)
+])
+def test_linear_fp8_tail_on_light_workgroups(O, dev, M, K, N, gelu, bias):
+    print(f"case linear fused tail {M}x{K}x{N} gelu={gelu} bias={bias}", flush=True)
+    rows = np.concatenate([np.arange(0, 64), np.arange(5000, 5064), np.arange(M - 320, M)])
+    _check_linear(O, dev, M, K, N, gelu, bias=bias, rows=rows)
+
+
+@pytest.mark.parametrize("M,K,N,act", [(300, 1024, 384, 1), (289, 4352, 256, 0), (33, 896, 128, 1),
+                                       (10785, 896, 4096, 1)])
 def test_gemm_tail_writes_nothing_past_m_or_n(dev, M, K, N, act):
     """Tail stripes (44, 33 and 33 rows; the last two on 8 and 4 waves) into a
     buffer with 64 guard rows and 8 guard columns (row stride N + 8): the
