@@ -1444,6 +1444,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_rowcol_oe_kernel(Params p) {
 // the persistent kernel's: bf16(acc sa sb + bias), GELU-tanh of that bf16
 // value, rounded to bf16; each thread stores 8 consecutive columns of one row
 // (16 bytes); rows past M are loaded as the last row and not stored.
+//
+// BLOCKWISE (the decoder's 128 x 128 block scales, gemm_bw8_kernel's
+// contract): a 128-byte K step is one scale block, and the stripe's rows and a
+// workgroup's 32 columns lie in one 128-row and one 128-column scale block, so
+// a wave adds each step's product times that block's factor
+// f_k = sa[mb][k] sb[nb][k] (skipped when f_k = 0), and the epilogue is
+// bf16(acc). The factors are read through the constant address space (scalar
+// loads, outside the vector-memory counter the DMA waits count).
 constexpr int TAIL_ROWS = 64;
 constexpr int TAIL_COLS = 32;
 constexpr int TAIL_STAGES = 3;
@@ -1454,7 +1462,7 @@ constexpr int tail_stage_bytes() { return (32 * JB + 32) * BK; }
 template <int SK, int JB>
 constexpr int tail_smem_bytes() { return SK * TAIL_STAGES * tail_stage_bytes<JB>(); }
 
-template <int ACT, int SK, int JB>
+template <int MODE, int ACT, int SK, int JB>
 __global__ __launch_bounds__(64 * SK) void gemm_tail_kernel(Params p, int64_t m0) {
     constexpr int AR = 32 * JB, NQ = (AR + 32) / 8, STG = tail_stage_bytes<JB>();
     static_assert(JB * 64 * 16 * 4 <= STG, "a wave's partial sums fit its stages");
@@ -1489,18 +1497,46 @@ __global__ __launch_bounds__(64 * SK) void gemm_tail_kernel(Params p, int64_t m0
     for (int j = 0; j < JB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+    typedef const __attribute__((address_space(4))) float cfloat;
+    cfloat* const sa_row = (cfloat*)p.sa + (m0 >> 7) * KT;  // BLOCKWISE: the stripe's scale row
+    cfloat* const sb_row = (cfloat*)p.sb + (n0 >> 7) * KT;  // and the columns' one
 #pragma unroll
     for (int d = 0; d < TAIL_STAGES; ++d) issue(d, d);
     int st = 0;
     for (int t = 0; t < T; ++t) {
+        float f = 1.0f;
+        if (MODE == BLOCKWISE) {
+            const int k = w + SK * t;
+            f = sa_row[k] * sb_row[k];
+        }
         // Step t's loads are the oldest in flight: (TAIL_STAGES - 1) NQ later ones may stay.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((TAIL_STAGES - 1) * NQ) : "memory");
         const uint8_t* const sb = ws + st * STG;
+        if (MODE == ROWCOL) {
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            const i32x8 fb = read_frag(sb, AR + (lane & 31), kh, lane);
+            for (int kh = 0; kh < 2; ++kh) {
+                const i32x8 fb = read_frag(sb, AR + (lane & 31), kh, lane);
 #pragma unroll
-            for (int j = 0; j < JB; ++j) acc[j] = mfma(fb, read_frag(sb, 32 * j + (lane & 31), kh, lane), acc[j]);
+                for (int j = 0; j < JB; ++j)
+                    acc[j] = mfma(fb, read_frag(sb, 32 * j + (lane & 31), kh, lane), acc[j]);
+            }
+        } else if (f != 0.0f) {
+            f32x16 blk[JB];
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) blk[j][v] = 0.0f;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh) {
+                const i32x8 fb = read_frag(sb, AR + (lane & 31), kh, lane);
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+                    blk[j] = mfma(fb, read_frag(sb, 32 * j + (lane & 31), kh, lane), blk[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[j][v] = fmaf(blk[j][v], f, acc[j][v]);
         }
         issue(st, t + TAIL_STAGES);
         st = st + 1 == TAIL_STAGES ? 0 : st + 1;
@@ -1536,6 +1572,11 @@ __global__ __launch_bounds__(64 * SK) void gemm_tail_kernel(Params p, int64_t m0
             y[4 * hh] = s.x; y[4 * hh + 1] = s.y; y[4 * hh + 2] = s.z; y[4 * hh + 3] = s.w;
         }
         const int64_t n = n0 + 8 * g;
+        if (MODE == BLOCKWISE) {
+            *reinterpret_cast<uint4*>(p.out + m * p.ldc + n) =
+                make_uint4(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]), pack_bf16(y[4], y[5]), pack_bf16(y[6], y[7]));
+            continue;
+        }
         const float sam = p.sa[m];
         const float4 sb0 = *reinterpret_cast<const float4*>(p.sb + n);
         const float4 sb1 = *reinterpret_cast<const float4*>(p.sb + n + 4);
@@ -1596,10 +1637,25 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
     HN_REQUIRE((M + gemm::BM - 1) / gemm::BM * ((N + 191) / 192) <= 0x7fffffffLL, HN_E_ARG,
                "FP8 GEMM: too many tiles");
     const bool persistent = mode == gemm::ROWCOL && K / gemm::BK >= gemm::O_MIN_KT;
-    // Persistent launches hand a last row stripe of at most TAIL_ROWS rows to
-    // gemm_tail_kernel and tile only the rows above it.
+    // A last row stripe of at most TAIL_ROWS rows goes to gemm_tail_kernel (or,
+    // in persistent launches, possibly to the light workgroups), and the tiles
+    // cover only the rows above it: always in persistent launches; in
+    // blockwise ones (one tile per workgroup, one workgroup per CU) when that
+    // saves a whole round of tiles (the decoder's gate and up projections,
+    // 10 800 x 4096 -> 12 288: 2064 tiles, 9 rounds, against 2016, 8) and K
+    // has at least 4 scale blocks (a K step for each of up to 4 waves).
     const int64_t m_tail = M % gemm::BM;
-    const int64_t Mt = persistent && m_tail <= gemm::TAIL_ROWS ? M - m_tail : M;
+    bool stripe = false;
+    if (m_tail > 0 && m_tail <= gemm::TAIL_ROWS) {
+        if (persistent) {
+            stripe = true;
+        } else if (mode == gemm::BLOCKWISE && K / gemm::BK >= 4) {
+            const int64_t cus = device_cus(), tn = (N + gemm::BN - 1) / gemm::BN;
+            const int64_t all = (M + gemm::BM - 1) / gemm::BM * tn, whole = M / gemm::BM * tn;
+            stripe = (all + cus - 1) / cus > (whole + cus - 1) / cus;
+        }
+    }
+    const int64_t Mt = stripe ? M - m_tail : M;
     const int64_t tm = (Mt + gemm::BM - 1) / gemm::BM;
     auto set_tiles = [&](int bn) {
         const gemm::TileCounts t = gemm::tile_counts(Mt, N, bn);
@@ -1622,8 +1678,12 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
         const hipStream_t st = (hipStream_t)stream;
         const bool two = m_tail > 32, four = N / gemm::TAIL_COLS < device_cus(), gelu = act == HN_ACT_GELU_TANH;
         const dim3 tblock(four ? 256 : 128);
-#define HN_TAIL(A, SK, JB) gemm::gemm_tail_kernel<A, SK, JB><<<tgrid, tblock, 0, st>>>(pt, Mt)
-        if (gelu) {
+#define HN_TAIL(A, SK, JB) gemm::gemm_tail_kernel<gemm::ROWCOL, A, SK, JB><<<tgrid, tblock, 0, st>>>(pt, Mt)
+#define HN_TAIL_BW(SK, JB) gemm::gemm_tail_kernel<gemm::BLOCKWISE, HN_ACT_NONE, SK, JB><<<tgrid, tblock, 0, st>>>(pt, Mt)
+        if (mode == gemm::BLOCKWISE) {
+            if (four) { if (two) HN_TAIL_BW(4, 2); else HN_TAIL_BW(4, 1); }
+            else { if (two) HN_TAIL_BW(2, 2); else HN_TAIL_BW(2, 1); }
+        } else if (gelu) {
             if (four) { if (two) HN_TAIL(HN_ACT_GELU_TANH, 4, 2); else HN_TAIL(HN_ACT_GELU_TANH, 4, 1); }
             else { if (two) HN_TAIL(HN_ACT_GELU_TANH, 2, 2); else HN_TAIL(HN_ACT_GELU_TANH, 2, 1); }
         } else {
@@ -1631,9 +1691,10 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
             else { if (two) HN_TAIL(HN_ACT_NONE, 2, 2); else HN_TAIL(HN_ACT_NONE, 2, 1); }
         }
 #undef HN_TAIL
+#undef HN_TAIL_BW
         return check_launch(who);
     };
-    if (persistent && Mt == 0) return launch_tail();
+    if (stripe && Mt == 0) return launch_tail();
     p.M = Mt;
     p.tail_M = Mt;
     if (persistent) {
@@ -1688,10 +1749,14 @@ static int gemm_launch(int mode, const void* a, const void* b, const float* sa, 
         } else {
             gemm::gemm_rowcol_oe_kernel<HN_ACT_NONE, 128><<<pgrid, gemm::NT, 0, st>>>(p);
         }
-    } else if (mode == gemm::ROWCOL)
+    } else if (mode == gemm::ROWCOL) {
         gemm::gemm_rowcol_kernel<<<grid, gemm::NT, 0, (hipStream_t)stream>>>(p);
-    else
+    } else {
+        if (stripe) {
+            if (const int rc = launch_tail(); rc != HN_OK) return rc;
+        }
         gemm::gemm_bw8_kernel<<<grid, gemm::NT8, 0, (hipStream_t)stream>>>(p);
+    }
     return check_launch(who);
 }
 

@@ -303,6 +303,39 @@ def test_blockwise_gemm_decoder_shapes(O, dev, m, n, k):
     _blockwise_check(got[rows], expected)
 
 
+# A blockwise launch whose last row stripe (at most 64 rows) would add a whole
+# round of tiles hands the stripe to gemm_tail_kernel in its blockwise mode:
+# the decoder's gate and up projections (10800 x 4096 -> 12288), 4116 rows
+# over 16 column tiles (257 -> 256 tiles), and M <= 64 (the stripe alone).
+# Activation K blocks of gains up to 2^+-8, an all-zero K block and zero
+# factors (a weight K block given scale 0, and the stripe's own row block).
+@pytest.mark.parametrize("m,n,k", [(10800, 12288, 4096), (4116, 4096, 512), (48, 512, 1024), (33, 256, 4096)])
+def test_blockwise_gemm_tail_stripe(O, dev, m, n, k):
+    print(f"case blockwise tail stripe {m}x{n}x{k}", flush=True)
+    pf = pkg_module("pixelumm_fp8")
+    g = torch.Generator().manual_seed(m + n)
+    a = torch.randn(m, k, generator=g)
+    b = torch.randn(n, k, generator=g)
+    gain = 2.0 ** torch.randint(-8, 9, (k // 128,), generator=g).float()
+    a = a * gain.repeat_interleave(128)[None, :]
+    a[:, 256:384] = 0.0
+    qa, sa = pf._quantize_blockwise(a.to(torch.bfloat16).to(dev))
+    qb, sb = pf._quantize_blockwise(b.to(torch.bfloat16).to(dev))
+    last = (m - 1) // 128
+    sb[0, 1] = 0.0        # a weight K block with factor 0 in the first column block
+    sa[last, 2] = 0.0     # and one in the stripe's own row block
+    got = pf.load_extension().gemm(qa, qb, sa, sb)
+    rows = sorted(set(range(0, min(m, 64))) | set(range(max(0, m - 96), m)))
+    rblocks = sorted(set(r // 128 for r in rows))
+    sa_sel = sa.cpu().numpy()[rblocks]
+    # re-index the selected rows' scale blocks for the oracle (rows in order, one scale row per 128)
+    expected = np.concatenate([
+        O.blockwise_gemm_reference(u8(qa)[[r for r in rows if r // 128 == rb]], sa_sel[[i]], u8(qb), sb.cpu().numpy())
+        for i, rb in enumerate(rblocks)])
+    _blockwise_check(got[rows], expected)
+    assert torch.equal(pf.load_extension().gemm(qa, qb, sa, sb), got)
+
+
 def test_blockwise_gemm_zero_block_factors(O, dev):
     """Block factors of 0 (an activation K block and a weight K block given scale 0
     by the caller) contribute nothing; the other blocks are promoted as usual."""
