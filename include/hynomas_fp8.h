@@ -133,7 +133,9 @@ int hn_kv_dequantize(int fmt, const void *q, const int64_t *qs, const float *sca
  * a/b/out 16-byte aligned, ldc % 8 == 0, N <= ldc <= 2^22.
  * Replaces F.linear(x, linear_weight(m), b) of the DiT block
  * (nomas_compile_prepost.py:45-47,80-87 via int8_stored_bf16_linear.py:82-100)
- * for FP8 weights, and the DeepGEMM per-token GEMM of fp8.py:27-38. */
+ * for FP8 weights, and the DeepGEMM per-token GEMM of fp8.py:27-38.
+ * Enqueues one kernel on `stream`, or two in order when the last row stripe
+ * (M % 256 <= 64 rows, K >= 896) gets a launch of its own; nothing else. */
 int hn_gemm_fp8_rowcol(const void *a, const void *b, const float *sa, const float *sb,
                        const void *bias, void *out, int64_t M, int64_t N, int64_t K,
                        int64_t ldc, int act, void *stream);
@@ -151,6 +153,10 @@ int hn_gemm_fp8_rowcol(const void *a, const void *b, const float *sa, const floa
  * FP8Linear loader refuses weight scale rows spanning more than 2^60
  * (pixelumm_fp8.validate_serialized_tensors); activation scales from the
  * blockwise quantizer span more only for bf16 blocks 2^60 apart in magnitude.
+ * When the last row stripe (M % 256 <= 64 rows) would add a round of tiles
+ * and K >= 512, its rows are computed by a second kernel enqueued first on
+ * the same stream, which adds each K block's product times its factor and
+ * has no such range limit.
  * Replaces gemm / pixel_gemm, hymm/models/vae/pixelumm_decoder/csrc/cutlass_fp8.cu:20-57
  * and reactor/hy_nomas_fp8_sm100.cu:67-107. */
 int hn_gemm_fp8_blockwise(const void *a, const void *b, const float *sa, const float *sb,
