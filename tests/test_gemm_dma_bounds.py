@@ -48,6 +48,7 @@ def test_the_checker_sees_uncapped_loads(checker):
 @pytest.mark.parametrize("M,N,K,SK,JB", [
     (10800, 12288, 3072, 2, 2), (10800, 3072, 12288, 4, 2), (257, 384, 1024, 2, 1), (288, 640, 896, 4, 1),
     (289, 512, 3072, 2, 2), (48, 1280, 3072, 4, 2), (1, 256, 4224, 4, 1), (64, 128, 896, 4, 2),
+    (276, 8192, 4224, 2, 1), (576, 8192, 4352, 2, 2),
     # blockwise stripes: the decoder's gate/up, 4116 rows (K 512: one K step per wave), M <= 64
     (10800, 12288, 4096, 2, 2), (4116, 4096, 512, 4, 1), (48, 512, 1024, 4, 2), (33, 256, 4096, 4, 2),
 ])

@@ -162,16 +162,19 @@ def test_linear_fp8_persistent_tiles(O, dev, M, K, N, gelu, bias):
 
 
 # A last row stripe of at most 64 rows (M % 256) goes to gemm_tail_kernel
-# (split-K over 4 waves, 8 past K = 4096; one or two 32-row blocks) while the
-# persistent kernel tiles the rows above it; M <= 64 runs the tail kernel
-# alone. Tails of 1, 32, 33, 48 and 64 rows, with and without GELU and bias.
+# (K split over 4 waves when the stripe has fewer 32-column groups than CUs,
+# else over 2; one or two 32-row blocks) while the persistent kernel tiles the
+# rows above it; M <= 64 runs the tail kernel alone. Tails of 1, 20, 32, 33,
+# 48 and 64 rows, with and without GELU and bias.
 @pytest.mark.parametrize("M,K,N,gelu,bias", [
     (257, 1024, 384, True, True),      # 1 tail row: one block, 4 waves
     (288, 896, 640, False, True),      # 32 tail rows: one block
     (289, 3072, 512, True, False),     # 33 tail rows: two blocks, no bias
     (48, 3072, 1280, True, True),      # tail only (no persistent launch)
-    (10800, 12288, 384, False, True),  # 48 tail rows, K 12288: 8 waves
+    (10800, 12288, 384, False, True),  # 48 tail rows, K 12288
     (1, 4224, 256, True, True),        # one row, K past 4096
+    (276, 4224, 8192, False, True),    # 20 tail rows, 256 column groups: K split over 2 waves
+    (576, 4352, 8192, True, True),     # 64 tail rows (two blocks), 2 waves, GELU
 ])
 def test_linear_fp8_tail_rows(O, dev, M, K, N, gelu, bias):
     print(f"case linear tail {M}x{K}x{N} gelu={gelu} bias={bias}", flush=True)
@@ -195,7 +198,7 @@ def test_linear_fp8_tail_on_light_workgroups(O, dev, M, K, N, gelu, bias):
 
 
 @pytest.mark.parametrize("M,K,N,act", [(300, 1024, 384, 1), (289, 4352, 256, 0), (33, 896, 128, 1),
-                                       (10785, 896, 4096, 1)])
+                                       (10785, 896, 4096, 1), (276, 4224, 8192, 0)])
 def test_gemm_tail_writes_nothing_past_m_or_n(dev, M, K, N, act):
     """Tail stripes (44, 33 and 33 rows; the last two on 8 and 4 waves) into a
     buffer with 64 guard rows and 8 guard columns (row stride N + 8): the
