@@ -355,29 +355,46 @@ def install_serialized_fp8(decoder: nn.Module, state: dict, metadata: dict, back
     modules, unchanged. The metadata must match PIXELUMM_HEADER and declare
     exactly those layers; every target must be a bias-free nn.Linear whose
     serialized tensors pass validate_serialized_tensors; every other tensor of
-    the state must be bf16. Returns the number of layers installed."""
-    from .pixelumm_fp8 import FP8Linear
+    the state must be bf16. Returns the number of layers installed.
+
+    The rules and their messages are the reference's
+    (pixelumm_decoder/prequantized.py:27-65), checked in the same order; here
+    every rule is checked, and every FP8Linear built, before the first layer
+    is replaced, so a refused file leaves the decoder as it was."""
     if backend not in PIXELUMM_BACKENDS:
         raise ValueError("Unsupported serialized PixelUMM FP8 backend: " + str(backend))
     if any(metadata.get(k) != v for k, v in PIXELUMM_HEADER.items()):
         raise ValueError("Unsupported PixelUMM FP8 checkpoint metadata")
-    targets = [f"layers.{i}.{p}" for i in range(len(decoder.layers)) for p in PIXELUMM_PROJECTIONS]
-    declared = json.loads(metadata.get("quantized_source_keys", "[]"))
-    wanted = {f"decoder.{t}.weight" for t in targets}
-    if (len(declared) != len(wanted) or set(declared) != wanted
-            or int(metadata.get("quantized_layers", -1)) != len(targets)):
-        raise ValueError("Incomplete or incompatible PixelUMM FP8 layer manifest")
-    for t in targets:
-        layer = decoder.get_submodule(t)
-        if not isinstance(layer, nn.Linear) or layer.bias is not None:
-            raise ValueError("Expected a bias-free PixelUMM linear: " + t)
-        fp8 = FP8Linear.from_quantized(state[t + ".fp8_weight"], state[t + ".fp8_scale"], layer.weight.shape)
-        owner, _, attr = t.rpartition(".")
-        setattr(decoder.get_submodule(owner), attr, fp8)
-    for key, tensor in state.items():
-        if not key.endswith((".fp8_weight", ".fp8_scale")) and tensor.dtype != torch.bfloat16:
-            raise ValueError("Expected BF16 unquantized tensor: " + key)
+    paths = [f"layers.{i}.{p}" for i in range(len(decoder.layers)) for p in PIXELUMM_PROJECTIONS]
+    _check_pixelumm_manifest(metadata, paths)
+    plan = [(path, _serialized_fp8_linear(decoder, state, path)) for path in paths]
+    stray = next((k for k, t in state.items()
+                  if not k.endswith((".fp8_weight", ".fp8_scale")) and t.dtype != torch.bfloat16), None)
+    if stray is not None:
+        raise ValueError("Expected BF16 unquantized tensor: " + stray)
+    for path, module in plan:
+        owner, _, attr = path.rpartition(".")
+        setattr(decoder.get_submodule(owner), attr, module)
     decoder._prequantized_fp8_backend = backend
     decoder._prequantized_fp8 = True
-    decoder._prequantized_fp8_layers = len(targets)
-    return len(targets)
+    decoder._prequantized_fp8_layers = len(plan)
+    return len(plan)
+
+
+def _check_pixelumm_manifest(metadata: dict, paths: list) -> None:
+    """The file's manifest names exactly the decoder's projection weights."""
+    declared = json.loads(metadata.get("quantized_source_keys", "[]"))
+    wanted = {f"decoder.{t}.weight" for t in paths}
+    if (len(declared) != len(wanted) or set(declared) != wanted
+            or int(metadata.get("quantized_layers", -1)) != len(paths)):
+        raise ValueError("Incomplete or incompatible PixelUMM FP8 layer manifest")
+
+
+def _serialized_fp8_linear(decoder: nn.Module, state: dict, path: str):
+    """The FP8Linear that replaces the bias-free nn.Linear at `path`, built
+    from its serialized codes and block scales (validated by from_quantized)."""
+    from .pixelumm_fp8 import FP8Linear
+    layer = decoder.get_submodule(path)
+    if not isinstance(layer, nn.Linear) or layer.bias is not None:
+        raise ValueError("Expected a bias-free PixelUMM linear: " + path)
+    return FP8Linear.from_quantized(state[path + ".fp8_weight"], state[path + ".fp8_scale"], layer.weight.shape)

@@ -289,6 +289,17 @@ def test_install_serialized_fp8(O, W, dev):
     bad_scale = dict(state, **{"layers.0.mlp.gate_proj.fp8_scale": -state["layers.0.mlp.gate_proj.fp8_scale"]})
     with pytest.raises(ValueError, match="positive"):
         W.install_serialized_fp8(fresh(), bad_scale, meta)
+    # a refusal found past the first layers (the last layer's scale, the bf16
+    # sweep) leaves every projection an nn.Linear and sets no attribute
+    last = "layers.1.attn.o_proj.fp8_scale"
+    for broken in (dict(state, **{last: -state[last]}),
+                   dict(state, **{"layers.1.norm.weight": torch.ones(256, device=dev)})):
+        d = fresh()
+        with pytest.raises(ValueError):
+            W.install_serialized_fp8(d, broken, meta)
+        assert all(type(d.get_submodule(f"layers.{i}.{p}")) is nn.Linear
+                   for i in range(2) for p in W.PIXELUMM_PROJECTIONS)
+        assert not hasattr(d, "_prequantized_fp8")
 
 
 class _Int8Stored(nn.Module):
